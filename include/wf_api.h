@@ -1,0 +1,105 @@
+/*
+ * wf_api.h - C ABI of libwf_mi355x.so, the gfx950 (MI355X) implementation of
+ * the quantized DiT-block path of the Wan2.1 block-causal denoiser:
+ *
+ *   - FP8 e4m3fn K/V packing into a paged, layer-wise KV pool, and the
+ *     gather-dequant of those pages;
+ *   - per-token int8 activation quantization and the W8A8 int8 GEMM
+ *     (i8 MFMA, int32 accumulation, per-channel dequant + bias, bf16 out);
+ *   - block-causal attention over the FP8 paged context.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer is a device pointer unless stated otherwise.  Tensors are
+ *     dense row-major; "bf16" buffers hold IEEE bfloat16 bit patterns.
+ *   - The library never allocates, frees or caches device memory.  Any
+ *     workspace is passed in by the caller.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Calls only
+ *     enqueue work; none of them synchronizes the device.
+ *   - Return value: 0 = success, > 0 = a hipError_t from the launch,
+ *     < 0 = a WF_E_* argument error.  wf_last_error() returns a
+ *     thread-local message describing the last non-zero status.
+ *   - Page tables are int32 device arrays of physical page ids.  Entries
+ *     outside [0, pool_pages) are skipped by the kernels (never written or
+ *     read), and callers are expected to validate them on the host.
+ */
+#ifndef WF_API_H
+#define WF_API_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WF_OK 0
+#define WF_E_INVALID (-1)     /* null pointer or negative size */
+#define WF_E_SHAPE (-2)       /* unsupported shape (e.g. head_dim != 128) */
+#define WF_E_ALIGN (-3)       /* pointer not aligned as required */
+
+/* ------------------------------------------------------------------ misc */
+
+/* Thread-local text of the last non-zero status returned on this thread. */
+const char* wf_last_error(void);
+
+/* ABI version: (major << 16) | minor. */
+int wf_abi_version(void);
+
+/* OCP e4m3fn round-to-nearest-even cast of n fp32 values, with the same
+ * results as torch's `x.to(torch.float8_e4m3fn)`: magnitudes that round
+ * above 448 and NaN become the NaN code 0x7f (sign kept), -0 keeps its sign.
+ * Replaces the elementwise casts at wave_rt/denoiser/exchange/common.py:150
+ * and wave_rt/denoiser/exchange/onesided.py:152 (scale == 1 case). */
+int wf_fp8_e4m3_encode_f32(const float* x, uint8_t* codes, int64_t n,
+                           void* stream);
+
+/* Exact e4m3fn -> fp32 decode of n codes (0x7f / 0xff decode to NaN).
+ * Replaces the upcast at wave_rt/denoiser/exchange/onesided.py:177-178. */
+int wf_fp8_e4m3_decode_f32(const uint8_t* codes, float* out, int64_t n,
+                           void* stream);
+
+/* ------------------------------------------------------- FP8 paged KV pool
+ *
+ * Pool layout (one pool for K, one for V):
+ *   codes  u8   [pool_pages][page_tokens][n_heads][head_dim]
+ *   scales f32  [pool_pages][n_heads][page_tokens]
+ * Logical token t of a packed sequence lives in physical page
+ * page_table[t / page_tokens], row t % page_tokens.
+ *
+ * Per (token, head) row x[0..head_dim):
+ *   s    = float( bf16( bf16(max|x|) / 448 ) ), then s = max(s, bf16(1e-8))
+ *   code = e4m3_rne( clamp( float(x) / s, -448, 448 ) )   (fp32 division)
+ * which is wave_rt/denoiser/exchange/common.py:145-150 with the amax taken
+ * per (token, head) in place of per tensor.
+ */
+
+/* Pack bf16 K and V [n_tokens][n_heads][head_dim] into the pools.
+ * `v` / `v_codes` / `v_scales` may all be NULL to pack K only.
+ * head_dim must be 128.  Replaces the quantize half of
+ * _all_gather_fp8 (wave_rt/denoiser/exchange/common.py:143-150) and the
+ * slot copies of _publish_paged (wave_rt/denoiser/exchange/paged.py:120-141)
+ * on a single GPU. */
+int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens,
+                   int32_t n_heads, int32_t head_dim,
+                   const int32_t* page_table, int64_t n_table,
+                   int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes,
+                   float* k_scales, float* v_scales, int64_t pool_pages,
+                   void* stream);
+
+/* Gather + dequantize the first n_tokens logical tokens of the pools back to
+ * bf16 [n_tokens][n_heads][head_dim]: out = bf16_rne(float(code) * s).
+ * `v_*` may be NULL to unpack K only.  Replaces the dequant of
+ * _all_gather_fp8 (wave_rt/denoiser/exchange/common.py:161-164, which
+ * yields fp32; here rounded once to bf16) and the context assembly of
+ * _make_denoise_exch_paged (wave_rt/denoiser/exchange/paged.py:215-247). */
+int wf_fp8_kv_unpack(const uint8_t* k_codes, const uint8_t* v_codes,
+                     const float* k_scales, const float* v_scales,
+                     int64_t pool_pages, const int32_t* page_table,
+                     int64_t n_table, int32_t page_tokens, int64_t n_tokens,
+                     int32_t n_heads, int32_t head_dim, void* k_out,
+                     void* v_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WF_API_H */

@@ -1,0 +1,57 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry
+point declared in include/wf_api.h, and rejects bad arguments with a status
+and message before touching the device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from waveforcing_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "wf_api.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(wf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert "wf_fp8_kv_pack" in names and len(names) >= 6
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_abi_version():
+    assert _lib.load().wf_abi_version() >> 16 == 1
+
+
+def test_bad_head_dim_is_rejected():
+    with pytest.raises(RuntimeError, match="head_dim=64"):
+        _lib.call("wf_fp8_kv_pack", 1, 2, 10, 2, 64, 3, 1, 16, 4, 5, 6, 7, 4, None)
+
+
+def test_short_page_table_is_rejected():
+    with pytest.raises(RuntimeError, match="page table covers"):
+        _lib.call("wf_fp8_kv_pack", 16, 32, 100, 2, 128, 48, 1, 16, 64, 80, 96, 112, 4, None)
+
+
+def test_negative_size_is_rejected():
+    with pytest.raises(RuntimeError, match="negative"):
+        _lib.call("wf_fp8_kv_unpack", 16, 32, 48, 64, 4, 80, 1, 16, -1, 2, 128, 96, 112, None)
+
+
+def test_unaligned_pointer_is_rejected():
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        _lib.call("wf_fp8_kv_pack", 17, 32, 10, 2, 128, 48, 1, 16, 64, 80, 96, 112, 4, None)
+
+
+def test_last_error_is_thread_local_text():
+    with pytest.raises(RuntimeError):
+        _lib.call("wf_fp8_e4m3_encode_f32", 0, 0, -5, None)
+    assert "n=-5" in _lib.last_error()

@@ -1,0 +1,92 @@
+"""ctypes binding of libwf_mi355x.so (the C ABI declared in include/wf_api.h).
+
+Every call goes through :func:`call`, which turns a non-zero status into a
+``RuntimeError`` carrying the library's thread-local message, the same way the
+reference's driver wrapper turns CUDA driver errors into ``RuntimeError``
+(wave_rt/distributed/ipc.py:28-37).  There is no fallback: if the library is
+missing or fails to load, every operation raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libwf_mi355x.so")
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+# name -> argtypes; pointers are passed as integers (device addresses).
+SIGNATURES: dict[str, list] = {
+    "wf_abi_version": [],
+    "wf_last_error": [],
+    "wf_fp8_e4m3_encode_f32": [_c_void_p, _c_void_p, _i64, _c_void_p],
+    "wf_fp8_e4m3_decode_f32": [_c_void_p, _c_void_p, _i64, _c_void_p],
+    "wf_fp8_kv_pack": [
+        _c_void_p, _c_void_p, _i64, _i32, _i32,
+        _c_void_p, _i64, _i32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+        _c_void_p,
+    ],
+    "wf_fp8_kv_unpack": [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+        _c_void_p, _i64, _i32, _i64, _i32, _i32,
+        _c_void_p, _c_void_p,
+        _c_void_p,
+    ],
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    """The HIP library has not been built (run ``python -m waveforcing_amd.build``)."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library with argument types installed."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise NativeLibraryMissing(
+                f"{LIB_PATH} not found; build it with `python -m waveforcing_amd.build`"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_char_p if name == "wf_last_error" else ctypes.c_int
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return load().wf_last_error().decode(errors="replace")
+
+
+def call(name: str, *args) -> None:
+    """Invoke ``name`` and raise ``RuntimeError`` on a non-zero status."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        raise RuntimeError(f"{name} failed (status {status}): {last_error()}")
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device=None) -> int:
+    """hipStream_t of torch's current stream on ``device``."""
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,185 @@
+"""FP8 e4m3fn paged KV pool on one GPU.
+
+The reference keeps per-(generation, layer) bf16 slabs of shape
+``(GT, Ln, Wmax*T, H, D)`` and fills fixed slots with DMA copies
+(wave_rt/denoiser/exchange/paged.py:43-48,120-145).  Its FP8 KV modes quantize
+per tensor (common.py:143-164) or cast without a scale (onesided.py:151-154),
+and paged mode rejects FP8 (paged.py:31-32).
+
+Here the slabs become one pool of physical pages per tensor (K and V), each
+page one latent frame of ``page_tokens`` tokens, stored as e4m3fn codes with
+one fp32 scale per (token, head):
+
+    codes  uint8   [pool_pages, page_tokens, H, D]
+    scales float32 [pool_pages, H, page_tokens]
+
+A logical token sequence (one layer's context) is a list of physical page
+ids.  With the identity page table and contiguous pages, page ``p`` holds
+slab rows ``[p*page_tokens, (p+1)*page_tokens)`` of the reference layout.
+The pool is allocated by the caller (like the reference's ``torch.zeros``
+slabs); the HIP kernels never allocate.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Sequence
+
+import torch
+
+from . import _lib, settings
+
+
+class PageTable:
+    """Validated page ids of one logical sequence, on host and device."""
+
+    def __init__(self, ids: Sequence[int], pool_pages: int, device) -> None:
+        host = [int(i) for i in ids]
+        for i in host:
+            if i < 0 or i >= pool_pages:
+                raise RuntimeError(f"page id {i} outside pool of {pool_pages} pages")
+        self.host = host
+        self.pool_pages = pool_pages
+        self.dev = torch.tensor(host, dtype=torch.int32, device=device)
+
+    def __len__(self) -> int:
+        return len(self.host)
+
+
+def _as_thd(x: torch.Tensor, name: str) -> torch.Tensor:
+    """Accept [T, H, D] or the reference's [1, T, H, D] views (paged.py:207-208)."""
+    if x.dim() == 4:
+        if x.shape[0] != 1:
+            raise ValueError(f"{name}: batch dimension must be 1, got {tuple(x.shape)}")
+        x = x[0]
+    if x.dim() != 3:
+        raise ValueError(f"{name}: expected [T, H, D], got {tuple(x.shape)}")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: expected bfloat16, got {x.dtype}")
+    return x.contiguous()
+
+
+class Fp8PagePool:
+    """K and V page pools in HBM with pack / gather-dequant through the HIP kernels."""
+
+    def __init__(
+        self,
+        pool_pages: int,
+        n_heads: int,
+        head_dim: int = settings.HEAD_DIM,
+        page_tokens: int = settings.PAGE_TOKENS,
+        device="cuda",
+    ) -> None:
+        if head_dim != 128:
+            raise ValueError(f"head_dim={head_dim} unsupported (kernels are specialised for 128)")
+        self.pool_pages = pool_pages
+        self.n_heads = n_heads
+        self.head_dim = head_dim
+        self.page_tokens = page_tokens
+        self.device = torch.device(device)
+        shape_c = (pool_pages, page_tokens, n_heads, head_dim)
+        shape_s = (pool_pages, n_heads, page_tokens)
+        self.k_codes = torch.zeros(shape_c, dtype=torch.uint8, device=self.device)
+        self.v_codes = torch.zeros(shape_c, dtype=torch.uint8, device=self.device)
+        self.k_scales = torch.zeros(shape_s, dtype=torch.float32, device=self.device)
+        self.v_scales = torch.zeros(shape_s, dtype=torch.float32, device=self.device)
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.k_codes, self.v_codes, self.k_scales, self.v_scales))
+
+    def page_table(self, ids: Sequence[int]) -> PageTable:
+        return PageTable(ids, self.pool_pages, self.device)
+
+    def pages_for(self, n_tokens: int) -> int:
+        return -(-n_tokens // self.page_tokens)
+
+    def pack(self, k: torch.Tensor, v: torch.Tensor | None, table: PageTable) -> None:
+        """Quantize K (and V) [T, H, D] bf16 into the pages listed by ``table``."""
+        k = _as_thd(k, "k")
+        if v is not None:
+            v = _as_thd(v, "v")
+            if v.shape != k.shape:
+                raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+        T, H, D = k.shape
+        if H != self.n_heads or D != self.head_dim:
+            raise ValueError(f"k has H={H}, D={D}; pool has H={self.n_heads}, D={self.head_dim}")
+        if len(table) * self.page_tokens < T:
+            raise RuntimeError(f"page table of {len(table)} pages cannot hold {T} tokens")
+        _lib.call(
+            "wf_fp8_kv_pack",
+            _lib.ptr(k), _lib.ptr(v), T, H, D,
+            table.dev.data_ptr(), len(table), self.page_tokens,
+            self.k_codes.data_ptr(), self.v_codes.data_ptr() if v is not None else None,
+            self.k_scales.data_ptr(), self.v_scales.data_ptr() if v is not None else None,
+            self.pool_pages,
+            _lib.stream_handle(self.device),
+        )
+
+    def unpack(
+        self,
+        table: PageTable,
+        n_tokens: int,
+        with_v: bool = True,
+        out_k: torch.Tensor | None = None,
+        out_v: torch.Tensor | None = None,
+    ):
+        """Gather + dequantize ``n_tokens`` logical tokens to bf16 [T, H, D]."""
+        if len(table) * self.page_tokens < n_tokens:
+            raise RuntimeError(f"page table of {len(table)} pages cannot hold {n_tokens} tokens")
+        shape = (n_tokens, self.n_heads, self.head_dim)
+        if out_k is None:
+            out_k = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
+        if with_v and out_v is None:
+            out_v = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
+        for name, t in (("out_k", out_k), ("out_v", out_v if with_v else None)):
+            if t is not None and (tuple(t.shape) != shape or t.dtype != torch.bfloat16 or not t.is_contiguous()):
+                raise ValueError(f"{name} must be contiguous bf16 {shape}")
+        _lib.call(
+            "wf_fp8_kv_unpack",
+            self.k_codes.data_ptr(), self.v_codes.data_ptr() if with_v else None,
+            self.k_scales.data_ptr(), self.v_scales.data_ptr() if with_v else None,
+            self.pool_pages, table.dev.data_ptr(), len(table), self.page_tokens,
+            n_tokens, self.n_heads, self.head_dim,
+            out_k.data_ptr(), out_v.data_ptr() if with_v else None,
+            _lib.stream_handle(self.device),
+        )
+        return (out_k, out_v) if with_v else out_k
+
+
+@dataclass
+class PagedKV:
+    """Page descriptor handed to the attention backend in place of dense K/V.
+
+    ``n_tokens`` logical keys live in ``pool`` at the pages of ``table``.
+    """
+
+    pool: Fp8PagePool
+    table: PageTable
+    n_tokens: int
+
+    @property
+    def shape(self):
+        # The reference reads ctx_k.shape[1] for its profile line (backend.py:151).
+        return (1, self.n_tokens, self.pool.n_heads, self.pool.head_dim)
+
+
+def fp8_encode(x: torch.Tensor) -> torch.Tensor:
+    """e4m3fn codes (uint8) of an fp32 device tensor: torch's ``x.to(float8_e4m3fn)``."""
+    if x.dtype != torch.float32:
+        raise ValueError("fp8_encode expects float32")
+    x = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    _lib.call("wf_fp8_e4m3_encode_f32", x.data_ptr(), out.data_ptr(), x.numel(), _lib.stream_handle(x.device))
+    return out
+
+
+def fp8_decode(codes: torch.Tensor) -> torch.Tensor:
+    """fp32 values of e4m3fn codes (uint8 device tensor)."""
+    if codes.dtype != torch.uint8:
+        raise ValueError("fp8_decode expects uint8 codes")
+    codes = codes.contiguous()
+    out = torch.empty(codes.shape, dtype=torch.float32, device=codes.device)
+    _lib.call("wf_fp8_e4m3_decode_f32", codes.data_ptr(), out.data_ptr(), codes.numel(),
+              _lib.stream_handle(codes.device))
+    return out
