@@ -98,6 +98,48 @@ int wf_fp8_kv_unpack(const uint8_t* k_codes, const uint8_t* v_codes,
                      int32_t n_heads, int32_t head_dim, void* k_out,
                      void* v_out, void* stream);
 
+/* ------------------------------------------------------------- W8A8 int8
+ *
+ * Per-token activation / per-output-channel weight symmetric int8 scheme,
+ * the int8 counterpart of WaveFp8Linear (wave_rt/runtime/fp8.py:21-61,
+ * which quantizes per tensor to e4m3).
+ */
+
+/* Per-row int8 quantization of bf16 x [m][k] (row stride ldx elements):
+ *   s[r] = max(max_c |x[r,c]| / 127, 1e-8)                 (fp32)
+ *   q    = clamp(round_half_even(x / s), -127, 127)        (IEEE fp32 x / s)
+ * q is dense int8 [m][k].  Used for activations (rows = tokens) and for
+ * weights (rows = output channels).  k % 16 == 0; x, q 16-byte aligned.
+ * Replaces the activation/weight quantization of WaveFp8Linear
+ * (wave_rt/runtime/fp8.py:33-35 weights, :47-48 activations). */
+int wf_quant_rows_i8(const void* x, int64_t m, int64_t k, int64_t ldx,
+                     int8_t* q, float* scales, void* stream);
+
+#define WF_GEMM_GELU_TANH 1
+
+/* int8 GEMM y[m][n] = bf16((float(acc) * sx[m]) * sw[n] + bias[n]) with
+ * acc = sum_k a[m,k] * w[n,k] (int32, exact), each fp32 step rounded
+ * separately.  a [m][k] and w [n][k] are int8 row-major (K contiguous);
+ * bias is bf16 [n] or NULL; y has row stride ldy elements.  If acc_out is
+ * non-NULL the int32 accumulators are also written ([m][n], dense).
+ * flags & WF_GEMM_GELU_TANH applies GELU(tanh) to the bf16-rounded result
+ * (nn.GELU(approximate='tanh') of the FFN, causal_model.py:342-344).
+ * k % 16 == 0, n % 4 == 0, ldy % 4 == 0.  Replaces the torch._scaled_mm call
+ * of WaveFp8Linear._raw (wave_rt/runtime/fp8.py:49-56). */
+int wf_gemm_i8(const int8_t* a, const int8_t* w, int64_t m, int64_t n,
+               int64_t k, const float* sx, const float* sw, const void* bias,
+               void* y, int64_t ldy, int32_t* acc_out, int32_t flags,
+               void* stream);
+
+/* Fused W8A8 linear: wf_quant_rows_i8 of x into the caller's workspace
+ * (ws_q int8 [m][k], ws_sx fp32 [m]) followed by wf_gemm_i8 against the
+ * pre-quantized weight (qw int8 [n][k], sw fp32 [n]).  The call contract of
+ * WaveFp8Linear.forward (wave_rt/runtime/fp8.py:58-61) on 2-D input. */
+int wf_w8a8_linear(const void* x, int64_t m, int64_t k, int64_t ldx,
+                   const int8_t* qw, const float* sw, const void* bias,
+                   int64_t n, void* y, int64_t ldy, int32_t flags,
+                   int8_t* ws_q, float* ws_sx, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

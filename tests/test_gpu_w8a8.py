@@ -1,0 +1,121 @@
+"""GPU parity of the int8 W8A8 path against the CPU oracle.
+
+Bars: int8 codes and fp32 scales bit-exact; int32 accumulators exact; bf16
+outputs bit-exact for the plain epilogue (same fp32 operation order), and
+within 1e-2 relative error (the stated tolerance) with the GELU-tanh
+epilogue, whose tanh differs between the GPU and CPU math libraries.
+"""
+
+import pytest
+import torch
+
+from oracle import linear as olin
+from waveforcing_amd import inputs
+from waveforcing_amd.fp8 import WaveW8A8Linear, _quant_rows_i8, gemm_i8, quantize_transformer_w8a8
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.mark.parametrize("M,K,seed", [(4680, 1536, 0), (1, 16, 1), (37, 48, 2), (300, 8960, 3), (5, 4112, 4),
+                                      (4680, 5120, 5)])
+def test_quant_rows_bit_exact(M, K, seed):
+    x = inputs.outlier_activations(M, K, seed=seed, chan_seed=seed + 10)
+    q, s = _quant_rows_i8(x.to(DEV))
+    oq, os_ = olin.i8_quant_rows(x)
+    assert torch.equal(s.cpu(), os_)
+    assert torch.equal(q.cpu(), oq)
+
+
+def test_quant_rows_exact_ties_and_zero_rows():
+    e = torch.tensor([-3.0, 0.0, 2.0, 5.0])
+    k = torch.arange(-64, 64, dtype=torch.float32)
+    rows = torch.cat([torch.full((4, 1), 127.0), (k[None, :] + 0.5).expand(4, -1), torch.zeros(4, 15)], 1)
+    rows = (rows * torch.pow(2.0, e)[:, None]).to(torch.bfloat16)
+    rows = torch.cat([rows, torch.zeros((2, rows.shape[1]), dtype=torch.bfloat16)])
+    q, s = _quant_rows_i8(rows.to(DEV))
+    oq, os_ = olin.i8_quant_rows(rows)
+    assert torch.equal(s.cpu(), os_) and torch.equal(q.cpu(), oq)
+
+
+def test_quant_rows_random_scale_ties():
+    """Quotients that land on k + 1/2 after fp32 rounding (non-power-of-two scales)."""
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randint(-254, 255, (2048, 256), generator=g).float() / 2).to(torch.bfloat16)
+    x[:, 0] = torch.linspace(1, 120, 2048).to(torch.bfloat16)
+    q, s = _quant_rows_i8(x.to(DEV))
+    oq, os_ = olin.i8_quant_rows(x)
+    assert torch.equal(s.cpu(), os_) and torch.equal(q.cpu(), oq)
+
+
+def _gemm_case(M, N, K, seed, bias=True, gelu=False):
+    x = inputs.outlier_activations(M, K, seed=seed, chan_seed=seed + 1)
+    w, b = inputs.linear_weights(N, K, w_seed=seed + 2, b_seed=seed + 3)
+    qx, sx = olin.i8_quant_rows(x)
+    qw, sw = olin.i8_quant_rows(w)
+    acc = torch.empty((M, N), dtype=torch.int32, device=DEV)
+    y = gemm_i8(qx.to(DEV), qw.to(DEV), sx.to(DEV), sw.to(DEV), b.to(DEV) if bias else None, gelu=gelu,
+                acc_out=acc)
+    oy, oacc = olin.i8_gemm(qx, qw, sx, sw, b if bias else None, gelu=gelu)
+    return y.cpu(), acc.cpu(), oy, oacc
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (4680, 1536, 1536),   # single 1.3B linear
+    (4680, 4608, 1536),   # fused QKV
+    (4680, 1536, 8960),   # fc_out
+    (1, 4, 16), (17, 132, 48), (300, 256, 1552), (513, 1540, 272),
+])
+def test_gemm_exact(M, N, K):
+    y, acc, oy, oacc = _gemm_case(M, N, K, seed=M + N + K)
+    assert torch.equal(acc, oacc)
+    assert torch.equal(y, oy)
+
+
+def test_gemm_no_bias_exact():
+    y, acc, oy, oacc = _gemm_case(700, 384, 512, seed=3, bias=False)
+    assert torch.equal(acc, oacc) and torch.equal(y, oy)
+
+
+def test_gemm_gelu_within_tolerance():
+    y, acc, oy, oacc = _gemm_case(4680, 8960, 1536, seed=11, gelu=True)
+    assert torch.equal(acc, oacc)
+    rel = (y.float() - oy.float()).norm() / oy.float().norm()
+    assert rel < 1e-2, float(rel)
+    assert float((y.float() - oy.float()).abs().max()) <= 2 ** -6 * float(oy.float().abs().max())
+
+
+def test_linear_module_matches_oracle():
+    x, w, b = inputs.linear_1p3b()
+    lin = WaveW8A8Linear(w.to(DEV), b.to(DEV))
+    y, none = lin(x.to(DEV).reshape(1, 4680, 1536))
+    assert none is None and y.shape == (1, 4680, 1536)
+    assert torch.equal(y.cpu().reshape(4680, 1536), olin.i8_linear(x, w, b))
+
+
+def test_module_swap_scopes():
+    class FFN(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.fc_in = torch.nn.Linear(64, 256)
+            self.act = torch.nn.GELU(approximate="tanh")
+            self.fc_out = torch.nn.Linear(256, 64)
+
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q = torch.nn.Linear(64, 64)
+            self.ffn = FFN()
+
+    class T(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.blocks = torch.nn.ModuleList([Block(), Block()])
+
+    t = T().to(DEV).to(torch.bfloat16)
+    assert quantize_transformer_w8a8(t, scope="ffn") == 4
+    assert isinstance(t.blocks[0].ffn.act, torch.nn.Identity) and t.blocks[0].ffn.fc_in.gelu
+    t2 = T().to(DEV).to(torch.bfloat16)
+    assert quantize_transformer_w8a8(t2, scope="all") == 6
+    with pytest.raises(ValueError):
+        quantize_transformer_w8a8(torch.nn.Linear(4, 4))

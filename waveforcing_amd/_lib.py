@@ -39,7 +39,18 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _c_void_p,
         _c_void_p,
     ],
+    "wf_quant_rows_i8": [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p],
+    "wf_gemm_i8": [
+        _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+        _c_void_p, _i64, _c_void_p, _i32, _c_void_p,
+    ],
+    "wf_w8a8_linear": [
+        _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+        _i64, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
+    ],
 }
+
+GEMM_GELU_TANH = 1
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -33,6 +33,10 @@ COMMON_FLAGS = [
     "-fno-gpu-rdc",
     "-Wall",
     "-Wno-unused-function",
+    # No implicit multiply-add contraction: elementwise fp32 follows the
+    # reference's operation order exactly; kernels write fmaf() where they
+    # want a fused multiply-add.
+    "-ffp-contract=off",
     # Packed FP32 VALU forms are kept out of the generated code.
     "-Xclang",
     "-target-feature",

@@ -5,9 +5,9 @@
 // is owned by an aligned group of 8 lanes, 16 values (32 B in, 16 B of
 // codes out) per lane, so every code store is one 16-byte vector store and a
 // wave writes 8 rows = 1 KiB of consecutive codes.  The per-row absmax is an
-// 8-lane DPP reduction.  Each workgroup of 256 threads owns 64 consecutive
-// rows (two rows per lane group), with both rows' loads issued before any
-// arithmetic.  blockIdx.y selects K (0) or V (1).
+// 8-lane DPP reduction.  Each workgroup of 256 threads owns 32 * ROWS
+// consecutive rows (ROWS rows per lane group), with all rows' loads issued
+// before any arithmetic.  blockIdx.y selects K (0) or V (1).
 //
 // Arithmetic per row, following wave_rt/denoiser/exchange/common.py:145-150
 // with the amax taken per (token, head):
@@ -28,7 +28,14 @@ namespace wf {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kRowsPerBlock = 64;  // 256 threads / 8 lanes per row * 2 rows per group
+// Launch shape (rows per 8-lane group, non-temporal hints), chosen by a
+// sweep on MI355X over rows {1, 2, 4, 8} x hints: one row per lane group
+// with streaming (non-temporal) stores is fastest for pack (5.8 TB/s over
+// 30 layers in one launch) and for unpack with streaming loads and stores.
+constexpr int kPackRows = 1;
+constexpr bool kPackNtLoad = false, kPackNtStore = true;
+constexpr int kUnpackRows = 1;
+constexpr bool kUnpackNtLoad = true, kUnpackNtStore = true;
 
 struct PoolView {
   uint8_t* codes;
@@ -87,29 +94,53 @@ __device__ inline float scale_from_amax(float amax) {
   return fmaxf(s, bf16_bits_to_f32(kScaleFloorBf16Bits));
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ inline uint4 ld16(const uint4* p) {
+  if constexpr (NT) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+  } else {
+    return *p;
+  }
+}
+
+template <bool NT>
+__device__ inline void st16(uint4* p, const uint4& v) {
+  if constexpr (NT) {
+    const u32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+  } else {
+    *p = v;
+  }
+}
+
+// ROWS rows per lane group; a workgroup owns 32 * ROWS consecutive rows.
+template <int ROWS, bool NT_LOAD, bool NT_STORE>
 __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ k, const uint4* __restrict__ v,
                                                       uint32_t n_rows, PageGeom geom, PoolView kpool,
                                                       PoolView vpool) {
   const uint4* __restrict__ src = blockIdx.y == 0 ? k : v;
   const PoolView pool = blockIdx.y == 0 ? kpool : vpool;
   const uint32_t lane8 = threadIdx.x & 7u;
-  const uint32_t row0 = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const uint32_t row0 = blockIdx.x * (32u * ROWS) + (threadIdx.x >> 3);
 
-  uint4 a[2], b[2];
+  uint4 a[ROWS], b[ROWS];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < ROWS; ++u) {
     const uint32_t r = row0 + 32u * u;
     if (r < n_rows) {
       const uint4* p = src + static_cast<int64_t>(r) * (kHeadDim / 8) + lane8 * 2;
-      a[u] = p[0];
-      b[u] = p[1];
+      a[u] = ld16<NT_LOAD>(p);
+      b[u] = ld16<NT_LOAD>(p + 1);
     } else {
       a[u] = make_uint4(0, 0, 0, 0);
       b[u] = a[u];
     }
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < ROWS; ++u) {
     const uint32_t r = row0 + 32u * u;
     const float amax = group8_max(absmax8(a[u], b[u]));
     const float s = scale_from_amax(amax);
@@ -121,7 +152,7 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ 
     c.w = quant4(b[u].z, b[u].w, s, rcp);
     int64_t code_row, scale_idx;
     if (r < n_rows && locate(geom, r, code_row, scale_idx)) {
-      reinterpret_cast<uint4*>(pool.codes + code_row * kHeadDim)[lane8] = c;
+      st16<NT_STORE>(reinterpret_cast<uint4*>(pool.codes + code_row * kHeadDim) + lane8, c);
       if (lane8 == 0) pool.scales[scale_idx] = s;
     }
   }
@@ -139,29 +170,30 @@ __device__ inline uint2 dequant4(uint32_t w, float s) {
   return make_uint2(__builtin_bit_cast(uint32_t, blo), __builtin_bit_cast(uint32_t, bhi));
 }
 
+template <int ROWS, bool NT_LOAD, bool NT_STORE>
 __global__ __launch_bounds__(256) void kv_unpack_kernel(PoolView kpool, PoolView vpool, uint32_t n_rows,
                                                         PageGeom geom, uint4* __restrict__ kout,
                                                         uint4* __restrict__ vout) {
   const PoolView pool = blockIdx.y == 0 ? kpool : vpool;
   uint4* __restrict__ dst = blockIdx.y == 0 ? kout : vout;
   const uint32_t lane8 = threadIdx.x & 7u;
-  const uint32_t row0 = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const uint32_t row0 = blockIdx.x * (32u * ROWS) + (threadIdx.x >> 3);
 
-  uint4 c[2];
-  float s[2];
-  bool ok[2];
+  uint4 c[ROWS];
+  float s[ROWS];
+  bool ok[ROWS];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < ROWS; ++u) {
     const uint32_t r = row0 + 32u * u;
     int64_t code_row = 0, scale_idx = 0;
     ok[u] = r < n_rows && locate(geom, r, code_row, scale_idx);
     if (ok[u]) {
-      c[u] = reinterpret_cast<const uint4*>(pool.codes + code_row * kHeadDim)[lane8];
+      c[u] = ld16<NT_LOAD>(reinterpret_cast<const uint4*>(pool.codes + code_row * kHeadDim) + lane8);
       s[u] = pool.scales[scale_idx];
     }
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < ROWS; ++u) {
     if (!ok[u]) continue;
     const uint32_t r = row0 + 32u * u;
     const uint2 o0 = dequant4(c[u].x, s[u]);
@@ -169,8 +201,8 @@ __global__ __launch_bounds__(256) void kv_unpack_kernel(PoolView kpool, PoolView
     const uint2 o2 = dequant4(c[u].z, s[u]);
     const uint2 o3 = dequant4(c[u].w, s[u]);
     uint4* p = dst + static_cast<int64_t>(r) * (kHeadDim / 8) + lane8 * 2;
-    p[0] = make_uint4(o0.x, o0.y, o1.x, o1.y);
-    p[1] = make_uint4(o2.x, o2.y, o3.x, o3.y);
+    st16<NT_STORE>(p, make_uint4(o0.x, o0.y, o1.x, o1.y));
+    st16<NT_STORE>(p + 1, make_uint4(o2.x, o2.y, o3.x, o3.y));
   }
 }
 
@@ -224,8 +256,9 @@ int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_hea
              WF_E_ALIGN, "%s: K/V and code pools must be 16-byte aligned", fn);
   const uint32_t n_rows = static_cast<uint32_t>(n_tokens * n_heads);
   const wf::PageGeom geom = wf::make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
-  const dim3 grid((n_rows + wf::kRowsPerBlock - 1) / wf::kRowsPerBlock, has_v ? 2 : 1);
-  hipLaunchKernelGGL(wf::kv_pack_kernel, grid, dim3(256), 0, wf::as_stream(stream),
+  constexpr int kRows = wf::kPackRows;
+  const dim3 grid((n_rows + 32 * kRows - 1) / (32 * kRows), has_v ? 2 : 1);
+  hipLaunchKernelGGL((wf::kv_pack_kernel<kRows, wf::kPackNtLoad, wf::kPackNtStore>), grid, dim3(256), 0, wf::as_stream(stream),
                      reinterpret_cast<const uint4*>(k), reinterpret_cast<const uint4*>(v), n_rows, geom,
                      wf::PoolView{k_codes, k_scales}, wf::PoolView{v_codes, v_scales});
   return wf::check_launch(fn);
@@ -246,8 +279,9 @@ int wf_fp8_kv_unpack(const uint8_t* k_codes, const uint8_t* v_codes, const float
              WF_E_ALIGN, "%s: outputs and code pools must be 16-byte aligned", fn);
   const uint32_t n_rows = static_cast<uint32_t>(n_tokens * n_heads);
   const wf::PageGeom geom = wf::make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
-  const dim3 grid((n_rows + wf::kRowsPerBlock - 1) / wf::kRowsPerBlock, has_v ? 2 : 1);
-  hipLaunchKernelGGL(wf::kv_unpack_kernel, grid, dim3(256), 0, wf::as_stream(stream),
+  constexpr int kRows = wf::kUnpackRows;
+  const dim3 grid((n_rows + 32 * kRows - 1) / (32 * kRows), has_v ? 2 : 1);
+  hipLaunchKernelGGL((wf::kv_unpack_kernel<kRows, wf::kUnpackNtLoad, wf::kUnpackNtStore>), grid, dim3(256), 0, wf::as_stream(stream),
                      wf::PoolView{const_cast<uint8_t*>(k_codes), const_cast<float*>(k_scales)},
                      wf::PoolView{const_cast<uint8_t*>(v_codes), const_cast<float*>(v_scales)}, n_rows, geom,
                      reinterpret_cast<uint4*>(k_out), reinterpret_cast<uint4*>(v_out));
