@@ -11,18 +11,23 @@
 // scale_b, + bias, bf16 out) and of the FFN's GELU(approximate='tanh')
 // (naive_rt/rolling_forcing/wan/modules/causal_model.py:342-344).
 //
-// Tiling: a 256-thread workgroup computes a 256 (M) x 128 (N) tile, K in
-// steps of 128 bytes.  Both operands are K-contiguous ("NT"), so global
-// loads are 16-byte vectors along K, staged through LDS (double buffered,
-// rows padded to 144 B so the 16-byte fragment reads of 8 consecutive rows
-// hit distinct banks).  The four waves form a 2 x 2 grid of 128 x 64 wave
-// tiles, each 4 x 2 blocks of v_mfma_i32_32x32x32_i8.  The weight fragment is
-// the MFMA's first operand and the activation fragment the second, so the
-// 32x32 result block is (n, m): each lane ends up with 4 consecutive output
-// features of one token per accumulator group, stored as one 8-byte bf16
-// vector.  Tiles are ordered so that the workgroups a given XCD receives
-// (blockIdx % 8) cover a contiguous band of M, keeping their activation rows
-// and the weight in that XCD's L2.
+// Tiling (template parameters; the launcher's choice is measured): a
+// workgroup computes a BM x BN tile with WM x WN waves, each wave a grid of
+// 32x32 v_mfma_i32_32x32x32_i8 blocks; K advances 128 bytes per step.  Both
+// operands are K-contiguous ("NT").  Global -> register staging uses buffer
+// loads (the descriptor range zero-fills rows past M/N, so loads carry no
+// predicate or branch) issued PGR steps ahead; LDS holds two stages with rows
+// padded to 144 B so the 16-byte fragment reads of 8 consecutive rows hit
+// distinct banks; each wave reads the fragments of sub-step s+1 while the
+// MFMAs of sub-step s run.  The weight fragment is the MFMA's first operand
+// and the activation fragment the second, so the 32x32 result block is
+// (n, m): each lane ends up with 4 consecutive output features of one token
+// per accumulator group, stored as one 8-byte bf16 vector.  Tiles are
+// ordered so that the workgroups one XCD receives (blockIdx % 8) form a
+// contiguous range, walked in bands of GROUP_M tile rows, so co-resident
+// workgroups share A and W panels in that XCD's L2.
+#include <utility>
+
 #include "launchers.hpp"
 #include "wf_common.hpp"
 
@@ -32,23 +37,32 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256, BN = 128, BK = 128;
-constexpr int PITCH = BK + 16;                 // LDS row pitch in bytes
-constexpr int A_STAGE = BM * PITCH;            // 36864 B
-constexpr int B_STAGE = BN * PITCH;            // 18432 B
-constexpr int STAGE = A_STAGE + B_STAGE;       // 55296 B
-constexpr int A_CHUNKS = BM * BK / 16 / 256;   // 16-byte loads per thread per stage (8)
-constexpr int B_CHUNKS = BN * BK / 16 / 256;   // (4)
+constexpr int BK = 128;
+// Word 3 of a raw (untyped, stride 0) buffer resource on gfx9-family parts:
+// DATA_FORMAT = 32 bit.  With it, offsets >= num_records read as zero.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kOutOfRange = 0x7ffffff0;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int PITCH = BK + 16;  // LDS row pitch in bytes
 constexpr int NUM_XCD = 8;
 
+template <int N, typename F, int... I>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
 struct GemmArgs {
-  const int8_t* a;     // [M, K]
-  const int8_t* w;     // [N, K]
-  const float* sx;     // [M]
-  const float* sw;     // [N]
+  const int8_t* a;       // [M, K]
+  const int8_t* w;       // [N, K]
+  const float* sx;       // [M]
+  const float* sw;       // [N]
   const uint16_t* bias;  // [N] bf16 or null
-  uint16_t* y;         // [M, N] bf16 (ldy)
-  int32_t* acc_out;    // [M, N] int32 or null
+  uint16_t* y;           // [M, N] bf16 (ldy)
+  int32_t* acc_out;      // [M, N] int32 or null
   int M, N, K;
   int64_t ldy;
 };
@@ -61,109 +75,173 @@ __device__ inline float gelu_tanh(float x) {
 
 __device__ inline float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_rne(f)); }
 
-template <bool HAS_BIAS, bool GELU>
-__global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs p) {
+// BM x BN workgroup tile, WM x WN waves, each wave (BM/WM) x (BN/WN) as
+// MI x NI blocks of 32x32.  OCC = waves per SIMD the register budget is
+// sized for (1: one workgroup of 4 waves per CU; 2: two).
+template <int BM, int BN, int WM, int WN, int OCC, int PGR, bool XCD_REMAP, int GROUP_M, bool HAS_BIAS, bool GELU>
+__global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_i8_kernel(GemmArgs p) {
+  constexpr int THREADS = WM * WN * 64;
+  constexpr int A_STAGE = BM * PITCH;
+  constexpr int B_STAGE = BN * PITCH;
+  constexpr int STAGE = A_STAGE + B_STAGE;
+  constexpr int A_CHUNKS = BM * BK / 16 / THREADS;
+  constexpr int B_CHUNKS = BN * BK / 16 / THREADS;
+  constexpr int MI = BM / WM / 32;
+  constexpr int NI = BN / WN / 32;
+  static_assert(A_CHUNKS * 16 * THREADS == BM * BK && B_CHUNKS * 16 * THREADS == BN * BK, "tile/threads");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
 
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (p.N + BN - 1) / BN;
   const int n_tiles = tiles_m * tiles_n;
-  const int per_xcd = (n_tiles + NUM_XCD - 1) / NUM_XCD;
-  const int t = (blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
+  int t = blockIdx.x;
+  if (XCD_REMAP) {
+    const int per_xcd = (n_tiles + NUM_XCD - 1) / NUM_XCD;
+    t = (blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
+  }
   if (t >= n_tiles) return;
-  const int m0 = (t / tiles_n) * BM;
-  const int n0 = (t % tiles_n) * BN;
+  int tm = t / tiles_n, tn = t % tiles_n;
+  if (GROUP_M > 0) {
+    // Grouped order: bands of GROUP_M tile rows swept column by column, so
+    // the workgroups resident on one XCD at a time form a compact block and
+    // share A rows and W rows in that XCD's L2.
+    const int per_group = GROUP_M * tiles_n;
+    const int first_m = (t / per_group) * GROUP_M;
+    const int rows = min(tiles_m - first_m, GROUP_M);
+    const int r = t % per_group;
+    tm = first_m + r % rows;
+    tn = r / rows;
+  }
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1;  // 0..1 -> 128-row half of the tile
-  const int wn = wave & 1;   // 0..1 -> 64-col half
+  const int wm = wave / WN;
+  const int wn = wave % WN;
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
-  // Global -> register staging of one K step.
-  uint4 ra[A_CHUNKS], rb[B_CHUNKS];
-  auto load_stage = [&](int k0) {
+  // Global -> register staging: PGR register buffers, so the loads of K
+  // step kb + PGR are issued while step kb computes and have PGR compute
+  // steps to arrive.  Buffer indices are compile-time (loop unrolled by PGR).
+  uint4 ra[PGR][A_CHUNKS], rb[PGR][B_CHUNKS];
+  // Buffer loads: the descriptor's range (M*K, N*K bytes) makes the hardware
+  // return zeros for rows past M / N, and K-tail chunks are pointed past the
+  // range, so the loads need no predicate and no branch.
+  const __amdgpu_buffer_rsrc_t rsrc_a =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), 0, p.M * p.K, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsrc_w =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), 0, p.N * p.K, kBufferRsrcWord3);
+  int off_a[A_CHUNKS], col_a[A_CHUNKS], off_b[B_CHUNKS], col_b[B_CHUNKS];
+#pragma unroll
+  for (int i = 0; i < A_CHUNKS; ++i) {
+    const int c = tid + THREADS * i;
+    col_a[i] = (c & 7) * 16;
+    off_a[i] = (m0 + (c >> 3)) * p.K + col_a[i];
+  }
+#pragma unroll
+  for (int i = 0; i < B_CHUNKS; ++i) {
+    const int c = tid + THREADS * i;
+    col_b[i] = (c & 7) * 16;
+    off_b[i] = (n0 + (c >> 3)) * p.K + col_b[i];
+  }
+  auto load_stage = [&](auto buf, int k0) {
+    constexpr int u = decltype(buf)::value;
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3, col = (c & 7) * 16;
-      const int gm = m0 + row, gk = k0 + col;
-      ra[i] = (gm < p.M && gk < p.K) ? *reinterpret_cast<const uint4*>(p.a + static_cast<int64_t>(gm) * p.K + gk)
-                                    : make_uint4(0, 0, 0, 0);
+      const int off = (k0 + col_a[i] < p.K) ? off_a[i] + k0 : kOutOfRange;
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, off, 0, 0);
+      ra[u][i] = make_uint4(v[0], v[1], v[2], v[3]);
     }
 #pragma unroll
     for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3, col = (c & 7) * 16;
-      const int gn = n0 + row, gk = k0 + col;
-      rb[i] = (gn < p.N && gk < p.K) ? *reinterpret_cast<const uint4*>(p.w + static_cast<int64_t>(gn) * p.K + gk)
-                                    : make_uint4(0, 0, 0, 0);
+      const int off = (k0 + col_b[i] < p.K) ? off_b[i] + k0 : kOutOfRange;
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, off, 0, 0);
+      rb[u][i] = make_uint4(v[0], v[1], v[2], v[3]);
     }
   };
-  auto store_stage = [&](int buf) {
-    uint8_t* sa = lds + buf * STAGE;
+  auto store_stage = [&](auto buf, int lbuf) {
+    constexpr int u = decltype(buf)::value;
+    uint8_t* sa = lds + lbuf * STAGE;
     uint8_t* sb = sa + A_STAGE;
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(sa + (c >> 3) * PITCH + (c & 7) * 16) = ra[i];
+      const int c = tid + THREADS * i;
+      *reinterpret_cast<uint4*>(sa + (c >> 3) * PITCH + (c & 7) * 16) = ra[u][i];
     }
 #pragma unroll
     for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(sb + (c >> 3) * PITCH + (c & 7) * 16) = rb[i];
+      const int c = tid + THREADS * i;
+      *reinterpret_cast<uint4*>(sb + (c >> 3) * PITCH + (c & 7) * 16) = rb[u][i];
     }
   };
 
-  v16i acc[2][4];  // [n block j][m block i]
+  v16i acc[NI][MI];  // [n block j][m block i]
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < NI; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[j][i] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < MI; ++i) acc[j][i] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  const int nk = (p.K + BK - 1) / BK;
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-
-  for (int kb = 0; kb < nk; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < nk) load_stage((kb + 1) * BK);
-    const uint8_t* sa = lds + cur * STAGE;
-    const uint8_t* sb = sa + A_STAGE;
+  auto compute = [&](int lbuf) {
+    const uint8_t* sa = lds + lbuf * STAGE + (wm * (BM / WM) + l32) * PITCH + half * 16;
+    const uint8_t* sb = lds + lbuf * STAGE + A_STAGE + (wn * (BN / WN) + l32) * PITCH + half * 16;
+    // Fragments of sub-step s + 1 are read while the MFMAs of sub-step s run.
+    v4i fa[2][MI], fw[2][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) fa[0][i] = *reinterpret_cast<const v4i*>(sa + i * 32 * PITCH);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) fw[0][j] = *reinterpret_cast<const v4i*>(sb + j * 32 * PITCH);
 #pragma unroll
     for (int s = 0; s < BK / 32; ++s) {
-      const int col = s * 32 + half * 16;
-      v4i fa[4], fw[2];
+      const int cb = s & 1;
+      if (s + 1 < BK / 32) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        fa[i] = *reinterpret_cast<const v4i*>(sa + (wm * 128 + i * 32 + l32) * PITCH + col);
+        for (int i = 0; i < MI; ++i)
+          fa[cb ^ 1][i] = *reinterpret_cast<const v4i*>(sa + i * 32 * PITCH + (s + 1) * 32);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        fw[j] = *reinterpret_cast<const v4i*>(sb + (wn * 64 + j * 32 + l32) * PITCH + col);
+        for (int j = 0; j < NI; ++j)
+          fw[cb ^ 1][j] = *reinterpret_cast<const v4i*>(sb + j * 32 * PITCH + (s + 1) * 32);
+      }
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NI; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[j][i], 0, 0, 0);
+        for (int i = 0; i < MI; ++i)
+          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[cb][j], fa[cb][i], acc[j][i], 0, 0, 0);
     }
-    if (kb + 1 < nk) store_stage(cur ^ 1);
-    __syncthreads();
+  };
+
+  // Steps past K load zeros (a zero contribution), so the step count is
+  // padded to a multiple of PGR and every step runs unconditionally.
+  const int nk = ((p.K + BK - 1) / BK + PGR - 1) / PGR * PGR;
+  static_for<PGR>([&](auto u) { load_stage(u, u.value * BK); });
+  store_stage(std::integral_constant<int, 0>{}, 0);
+  __syncthreads();
+
+  for (int kb0 = 0; kb0 < nk; kb0 += PGR) {
+    static_for<PGR>([&](auto u) {
+      constexpr int U = decltype(u)::value;
+      const int kb = kb0 + U;
+      // register buffer U held step kb, already in LDS: refill it with step kb + PGR
+      load_stage(u, (kb + PGR) * BK);
+      compute(kb & 1);
+      store_stage(std::integral_constant<int, (U + 1) % PGR>{}, (kb + 1) & 1);
+      __syncthreads();
+    });
   }
 
   // Epilogue.  Block (j, i) element (n, m): m = l32, n = 8*(r/4) + 4*half + r%4.
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int gm = m0 + wm * 128 + i * 32 + l32;
+  for (int i = 0; i < MI; ++i) {
+    const int gm = m0 + wm * (BM / WM) + i * 32 + l32;
     const bool row_ok = gm < p.M;
     const float sxm = row_ok ? p.sx[gm] : 0.f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NI; ++j) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int gn = n0 + wn * 64 + j * 32 + 8 * g + 4 * half;
+        const int gn = n0 + wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
         // N % 4 == 0 (checked at the entry point): a 4-wide group is all in or all out.
         if (row_ok && gn < p.N) {
           const int a0 = acc[j][i][4 * g + 0], a1 = acc[j][i][4 * g + 1];
@@ -198,11 +276,24 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_kernel(GemmArgs p) {
   }
 }
 
-}  // namespace
+template <int BM, int BN, int WM, int WN, int OCC, int PGR, bool XCD_REMAP, int GROUP_M>
+int launch_cfg(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream) {
+  const int64_t tiles = ((static_cast<int64_t>(p.M) + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  const int64_t grid = XCD_REMAP ? (tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD : tiles;
+  const dim3 g(static_cast<uint32_t>(grid)), b(WM * WN * 64);
+  if (bias && gelu)
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, OCC, PGR, XCD_REMAP, GROUP_M, true, true>), g, b, 0, stream, p);
+  else if (bias)
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, OCC, PGR, XCD_REMAP, GROUP_M, true, false>), g, b, 0, stream, p);
+  else if (gelu)
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, OCC, PGR, XCD_REMAP, GROUP_M, false, true>), g, b, 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, OCC, PGR, XCD_REMAP, GROUP_M, false, false>), g, b, 0, stream, p);
+  return check_launch("wf_gemm_i8");
+}
 
-int launch_gemm_i8(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64_t K, const float* sx,
-                   const float* sw, const void* bias, void* y, int64_t ldy, int32_t* acc_out, int gelu,
-                   hipStream_t stream) {
+GemmArgs make_args(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64_t K, const float* sx,
+                   const float* sw, const void* bias, void* y, int64_t ldy, int32_t* acc_out) {
   GemmArgs p;
   p.a = a;
   p.w = w;
@@ -215,18 +306,20 @@ int launch_gemm_i8(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64
   p.N = static_cast<int>(N);
   p.K = static_cast<int>(K);
   p.ldy = ldy;
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const int64_t grid = (tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
-  const dim3 g(static_cast<uint32_t>(grid)), b(256);
-  if (bias && gelu)
-    hipLaunchKernelGGL((gemm_i8_kernel<true, true>), g, b, 0, stream, p);
-  else if (bias)
-    hipLaunchKernelGGL((gemm_i8_kernel<true, false>), g, b, 0, stream, p);
-  else if (gelu)
-    hipLaunchKernelGGL((gemm_i8_kernel<false, true>), g, b, 0, stream, p);
-  else
-    hipLaunchKernelGGL((gemm_i8_kernel<false, false>), g, b, 0, stream, p);
-  return check_launch("wf_gemm_i8");
+  return p;
+}
+
+}  // namespace
+
+int launch_gemm_i8(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64_t K, const float* sx,
+                   const float* sw, const void* bias, void* y, int64_t ldy, int32_t* acc_out, int gelu,
+                   hipStream_t stream) {
+  const GemmArgs p = make_args(a, w, M, N, K, sx, sw, bias, y, ldy, acc_out);
+  // 128 x 256 tiles, 2 x 4 waves of 64 x 64, two workgroups per CU, loads
+  // two K steps ahead, XCD-contiguous grouped order (bands of 8 tile rows):
+  // the best of a sweep over tile shape, waves, occupancy, prefetch depth and
+  // rasterization on the Wan-1.3B/14B linear shapes.
+  return launch_cfg<128, 256, 2, 4, 2, 2, true, 8>(p, bias != nullptr, gelu != 0, stream);
 }
 
 }  // namespace wf
@@ -239,7 +332,8 @@ extern "C" int wf_gemm_i8(const int8_t* a, const int8_t* w, int64_t m, int64_t n
              (long long)m, (long long)n, (long long)k, (long long)ldy);
   if (m == 0 || n == 0) return WF_OK;
   WF_REQUIRE(a && w && sx && sw && y, WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), WF_E_SHAPE, "%s: size exceeds 2^31", fn);
+  WF_REQUIRE((m + 256) * k < (1ll << 31) - 16 && (n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE,
+             "%s: operands of 2 GiB or more are not supported", fn);
   WF_REQUIRE(k % 16 == 0 && k > 0, WF_E_SHAPE, "%s: k=%lld must be a positive multiple of 16", fn, (long long)k);
   WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);
   WF_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
@@ -259,7 +353,8 @@ extern "C" int wf_w8a8_linear(const void* x, int64_t m, int64_t k, int64_t ldx, 
              (long long)ldx, (long long)ldy);
   if (m == 0 || n == 0) return WF_OK;
   WF_REQUIRE(x && qw && sw && y && ws_q && ws_sx, WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), WF_E_SHAPE, "%s: size exceeds 2^31", fn);
+  WF_REQUIRE((m + 256) * k < (1ll << 31) - 16 && (n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE,
+             "%s: operands of 2 GiB or more are not supported", fn);
   WF_REQUIRE(k % 16 == 0 && ldx % 8 == 0, WF_E_SHAPE, "%s: k %% 16 and ldx %% 8 must be 0", fn);
   WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);
   WF_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(qw) & 15u) == 0 &&
