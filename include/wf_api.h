@@ -140,6 +140,26 @@ int wf_w8a8_linear(const void* x, int64_t m, int64_t k, int64_t ldx,
                    int64_t n, void* y, int64_t ldy, int32_t flags,
                    int8_t* ws_q, float* ws_sx, void* stream);
 
+/* ------------------------------------------------------------- attention */
+
+/* Attention of bf16 queries q [lq][n_heads][128] (token stride ldq
+ * elements) over the first n_kv logical keys of the FP8 paged pools (layout
+ * as for wf_fp8_kv_pack), non-causal within the context:
+ *   out[q,h,:] = softmax_j(softmax_scale * <q[q,h,:], K[j,h,:]>) . V[j,h,:]
+ * with K = code_k * s_k and V = code_v * s_v per (key, head); fp32
+ * accumulation, bf16 out [lq][n_heads][128] (token stride ldo).
+ * page_tokens >= 64; each code pool < 2 GiB.  Replaces the attention
+ * dispatch of the patched self-attention (wave_rt/runtime/backend.py:141-148:
+ * fa_func / sageattn / SDPA over the paged context views of
+ * wave_rt/denoiser/exchange/paged.py:246-247). */
+int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads,
+                      int32_t head_dim, int64_t ldq, const uint8_t* k_codes,
+                      const uint8_t* v_codes, const float* k_scales,
+                      const float* v_scales, int64_t pool_pages,
+                      int32_t page_tokens, const int32_t* page_table,
+                      int64_t n_table, int64_t n_kv, float softmax_scale,
+                      void* out, int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,137 @@
+"""Attention-backend registry and the patched self-attention step.
+
+Mirrors the process-global state and backend switches of
+wave_rt/runtime/backend.py:18-62 (``_WAVE_STATE``, ``set_exchange_fn``,
+``enable_fa_custom``/``enable_sage``) and the attention part of its patched
+``CausalWanSelfAttention.forward`` (backend.py:102-157): RoPE'd q/k go to the
+installed exchange closure, which returns the context, then the selected
+attention kernel runs non-causally over it.
+
+The HIP backend, ``hip_fp8``, takes the context as a page descriptor
+(:class:`waveforcing_amd.kv.PagedKV`) that the paged FP8 exchange returns in
+place of the dense ``Kb[:active_len]`` views (paged.py:246-247), and runs
+``wf_attn_paged_fp8`` on it.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from typing import Callable
+
+import torch
+
+from . import _lib
+from .kv import PagedKV
+
+ATTENTION_BACKENDS = ("torch_sdpa", "fa_custom", "sa", "fa", "fa2", "hip_fp8")
+
+_WAVE_STATE: dict = {
+    "exchange_fn": None,
+    "attn": "torch_sdpa",
+    "fa_func": None,
+    "layer_prof_sink": None,
+}
+
+
+def set_exchange_fn(fn: Callable | None) -> None:
+    _WAVE_STATE["exchange_fn"] = fn
+
+
+def set_layer_prof_sink(sink) -> None:
+    """Set the optional sink for attention completion events."""
+    _WAVE_STATE["layer_prof_sink"] = sink
+
+
+def prof_reset(on: bool) -> None:
+    _WAVE_STATE["prof"] = on
+    _WAVE_STATE["attn_ms"] = 0.0
+    _WAVE_STATE["exch_ms"] = 0.0
+
+
+def prof_read() -> tuple:
+    return (_WAVE_STATE.get("attn_ms", 0.0), _WAVE_STATE.get("exch_ms", 0.0), _WAVE_STATE.get("klen", 0))
+
+
+def attn_paged_fp8(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, causal: bool = False,
+                   softmax_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """flash_attn_func-shaped call: q [1, Lq, H, D] (or [Lq, H, D]) bf16 over a paged FP8 context.
+
+    ``k`` carries both pools; ``v`` is accepted for call compatibility and
+    must be ``k`` itself or None.  Returns bf16 with q's shape.
+    """
+    if causal:
+        raise ValueError("the wavefront attention is non-causal over the context (backend.py:141-148)")
+    if not isinstance(k, PagedKV) or (v is not None and v is not k):
+        raise TypeError("hip_fp8 attention takes the PagedKV descriptor returned by the paged exchange")
+    squeeze = q.dim() == 4
+    q3 = q[0] if squeeze else q
+    if q3.dim() != 3 or q3.dtype != torch.bfloat16:
+        raise ValueError(f"q must be bf16 [1, Lq, H, D] or [Lq, H, D], got {tuple(q.shape)} {q.dtype}")
+    Lq, H, D = q3.shape
+    pool = k.pool
+    if H != pool.n_heads or D != pool.head_dim:
+        raise ValueError(f"q heads/dim ({H}, {D}) differ from the pool ({pool.n_heads}, {pool.head_dim})")
+    if q3.stride(2) != 1 or q3.stride(1) != D or q3.data_ptr() % 16 or q3.stride(0) % 8:
+        q3 = q3.contiguous()
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    o = out if out is not None else torch.empty((Lq, H, D), dtype=torch.bfloat16, device=q3.device)
+    if o.dim() == 4:
+        o = o[0]
+    _lib.call(
+        "wf_attn_paged_fp8", q3.data_ptr(), Lq, H, D, q3.stride(0),
+        pool.k_codes.data_ptr(), pool.v_codes.data_ptr(), pool.k_scales.data_ptr(), pool.v_scales.data_ptr(),
+        pool.pool_pages, pool.page_tokens, k.table.dev.data_ptr(), len(k.table), k.n_tokens,
+        float(softmax_scale), o.data_ptr(), o.stride(0), _lib.stream_handle(q3.device),
+    )
+    return o.unsqueeze(0) if squeeze else o
+
+
+def enable_hip_fp8() -> None:
+    """Use the gfx950 paged-FP8 attention on the wavefront path."""
+    _WAVE_STATE["attn"] = "hip_fp8"
+    _WAVE_STATE["fa_func"] = attn_paged_fp8
+
+
+def attend(roped_query, ctx_k, ctx_v, sdpa: Callable | None = None):
+    """Attention dispatch of the patched forward (backend.py:141-148)."""
+    attn = _WAVE_STATE["attn"]
+    if attn == "hip_fp8":
+        return _WAVE_STATE["fa_func"](roped_query, ctx_k, ctx_v, causal=False)
+    if attn == "fa_custom":
+        return _WAVE_STATE["fa_func"](roped_query, ctx_k, ctx_v, causal=False)
+    if attn == "sa":
+        return _WAVE_STATE["fa_func"](roped_query, ctx_k, ctx_v, tensor_layout="NHD", is_causal=False)
+    if sdpa is None:
+        raise RuntimeError(f"attention backend {attn!r} needs the model's own attention callable")
+    return sdpa(roped_query, ctx_k, ctx_v)
+
+
+def exchange_and_attend(layer_idx: int, roped_query, roped_key, unroped_key, value, sdpa: Callable | None = None,
+                        **geometry):
+    """The body of the patched self-attention after RoPE (backend.py:122-157)."""
+    exch = _WAVE_STATE["exchange_fn"]
+    if exch is None:
+        raise RuntimeError("no exchange function installed (set_exchange_fn)")
+    profiled = bool(_WAVE_STATE.get("prof"))
+    if profiled:
+        torch.cuda.synchronize()
+        started = time.perf_counter()
+    ctx_k, ctx_v = exch(layer_idx=layer_idx, roped_query=roped_query, roped_key=roped_key,
+                        unroped_key=unroped_key, value=value, **geometry)
+    if profiled:
+        torch.cuda.synchronize()
+        _WAVE_STATE["exch_ms"] = _WAVE_STATE.get("exch_ms", 0.0) + (time.perf_counter() - started) * 1000
+        started = time.perf_counter()
+    out = attend(roped_query, ctx_k, ctx_v, sdpa)
+    if profiled:
+        torch.cuda.synchronize()
+        _WAVE_STATE["attn_ms"] = _WAVE_STATE.get("attn_ms", 0.0) + (time.perf_counter() - started) * 1000
+        _WAVE_STATE["klen"] = ctx_k.shape[1]
+    sink = _WAVE_STATE.get("layer_prof_sink")
+    if sink is not None:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        sink.append(ev)
+    return out

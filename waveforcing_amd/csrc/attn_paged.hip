@@ -1,0 +1,384 @@
+// Block-causal attention over the FP8 paged KV context (bf16 matrix cores).
+//
+//   out[q, h, :] = softmax_j( scale * <Q[q,h,:], K[j,h,:]> ) . V[j,h,:]
+//   K[j,h,:] = code_k[j,h,:] * s_k[j,h],  V likewise (e4m3fn codes, fp32 scales)
+//
+// over the n_kv logical keys of a page table, with no mask inside the context:
+// the reference's wavefront attention is non-causal (backend.py:141-148,
+// causal=False) and block causality comes from which chunks the exchange
+// puts into the context.  Restates the attention the reference dispatches
+// (flash_attn_func / sageattn / SDPA, backend.py:141-148; the SDPA fallback
+// naive_rt/rolling_forcing/wan/modules/attention.py:75-89) on the FP8 pages
+// that replace the bf16 slab views of paged.py:246-247.
+//
+// Work split: a workgroup of 4 waves owns 128 queries of one head; each wave
+// owns 32 queries.  Keys advance in tiles of 64.  Per tile the workgroup
+// loads the K and V codes of the tile (through buffer descriptors over the
+// pools: keys past n_kv or on invalid pages read as zero) and the per-key
+// scales, decodes the codes once to bf16 (exact) into LDS, K as [key][d] and
+// V transposed as [d][key'] with the key order permuted within each group of
+// 16 (key bits 2 and 3 swapped) so that the PV operand fragment is one
+// 16-byte read that matches the register layout of P.
+//
+// The score block is computed transposed, S^T = K Q^T with
+// v_mfma_f32_32x32x16_bf16 (K fragment first operand, Q^T fragment second,
+// Q^T kept in registers for the whole kernel): each lane then holds one
+// query column and 16 keys per 32-key block, so the online-softmax row max
+// is an in-lane max plus one exchange with lane ^ 32, and the lane's P values
+// are directly the second operand of O^T = V^T P^T.  s_k (times
+// scale * log2 e) scales S^T rows, s_v scales P^T rows before the bf16
+// rounding of P; the row sum uses the unscaled P.
+#include <utility>
+
+#include "fastdiv.hpp"
+#include "fp8_codec.hpp"
+#include "wf_common.hpp"
+
+namespace wf {
+namespace {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int D = 128;
+constexpr int BQ = 128;          // queries per workgroup (4 waves x 32)
+constexpr int BKV = 64;          // keys per tile
+constexpr int KP = D * 2 + 16;   // K tile row pitch (bytes, bf16 + pad) = 272
+constexpr int VP = BKV * 2 + 16; // V^T tile row pitch (bytes) = 144
+constexpr int K_TILE = BKV * KP;
+constexpr int V_TILE = D * VP;
+constexpr int S_TILE = 2 * BKV * 4;  // c*s_k then s_v (fp32)
+constexpr int STAGE = K_TILE + V_TILE + S_TILE;
+constexpr int kBufferRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+constexpr int kOutOfRange = 0x7ffffff0;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+  const uint16_t* q;  // bf16 [Lq, ldq_tok] with head h at offset h * D
+  int64_t ldq;        // elements between consecutive query tokens
+  const uint8_t* k_codes;
+  const uint8_t* v_codes;
+  const float* k_scales;
+  const float* v_scales;
+  const int32_t* table;
+  uint16_t* out;  // bf16 [Lq, ldo] with head h at offset h * D
+  int64_t ldo;
+  int Lq, H, n_kv, n_table, page_tokens, pool_pages;
+  FastDiv page_div;
+  float qk_scale;  // softmax scale * log2(e)
+};
+
+// Two fp32 holding e4m3-exact values -> packed bf16x2 (truncation is exact).
+__device__ inline uint32_t f32x2_to_bf16x2_exact(float lo, float hi) {
+  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
+}
+
+// Decode 4 e4m3 codes (bytes of w) into 2 dwords of packed bf16.
+__device__ inline uint2 decode4_bf16(uint32_t w) {
+  float a, b, c, d;
+  e4m3_unpack4_hw(w, a, b, c, d);
+  return make_uint2(f32x2_to_bf16x2_exact(a, b), f32x2_to_bf16x2_exact(c, d));
+}
+
+__global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+  const int h = blockIdx.y;
+  const int q0 = blockIdx.x * BQ;
+
+  const int64_t pool_bytes = static_cast<int64_t>(p.pool_pages) * p.page_tokens * p.H * D;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.k_codes), 0,
+                                                                      static_cast<int>(pool_bytes), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.v_codes), 0,
+                                                                      static_cast<int>(pool_bytes), kBufferRsrcWord3);
+  const int scale_bytes = p.pool_pages * p.H * p.page_tokens * 4;
+  const __amdgpu_buffer_rsrc_t rsk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.k_scales), 0, scale_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.v_scales), 0, scale_bytes, kBufferRsrcWord3);
+
+  // A 64-key tile spans at most two pages (page_tokens >= 64, checked on
+  // the host): resolve them once per tile, then each key is a compare.
+  int tile_page0 = -1, tile_page1 = -1, tile_rip0 = 0, tile_t0 = 0;
+  auto map_tile = [&](int t0) {
+    uint32_t lp, rip;
+    p.page_div.divmod(static_cast<uint32_t>(t0), lp, rip);
+    tile_t0 = t0;
+    tile_rip0 = static_cast<int>(rip);
+    const int pg0 = static_cast<int>(lp) < p.n_table ? p.table[lp] : -1;
+    const int pg1 = static_cast<int>(lp) + 1 < p.n_table ? p.table[lp + 1] : -1;
+    tile_page0 = (pg0 >= 0 && pg0 < p.pool_pages) ? pg0 : -1;
+    tile_page1 = (pg1 >= 0 && pg1 < p.pool_pages) ? pg1 : -1;
+  };
+  // Byte offsets of (key t0 + k, head h, d = 0) in a code pool and of its
+  // scale; out of range for keys past n_kv or on invalid pages.
+  auto key_offsets = [&](int k, int& code_off, int& scale_off) {
+    int r = tile_rip0 + k;
+    int page = tile_page0;
+    if (r >= p.page_tokens) {
+      r -= p.page_tokens;
+      page = tile_page1;
+    }
+    const bool ok = page >= 0 && tile_t0 + k < p.n_kv;
+    code_off = ok ? ((page * p.page_tokens + r) * p.H + h) * D : kOutOfRange;
+    scale_off = ok ? ((page * p.H + h) * p.page_tokens + r) * 4 : kOutOfRange;
+  };
+
+  // ---- per-thread staging of one K/V tile ----------------------------------
+  // K: 2 x 16 codes (key = c / 8, d0 = 16 * (c % 8)), c = tid + 256 * i.
+  // V: 2 tasks of 4 keys x 4 d (dword loads), task = tid + 256 * i:
+  //    key group kg = task / 32 (keys 4kg..4kg+3), d = 4 * (task % 32).
+  // Scales: threads 0..63 load s_k of key tid, 64..127 s_v of key tid - 64.
+  u32x4 rk_code[2];
+  uint32_t rv_code[2][4];
+  float rscale;
+
+  auto load_tile = [&](int t0) {
+    map_tile(t0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;
+      int co, so;
+      key_offsets(c >> 3, co, so);
+      rk_code[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, co == kOutOfRange ? co : co + (c & 7) * 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int task = tid + 256 * i;
+      const int kg = task >> 5, d0 = (task & 31) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int co, so;
+        key_offsets(4 * kg + j, co, so);
+        rv_code[i][j] = __builtin_amdgcn_raw_buffer_load_b32(rv, co == kOutOfRange ? co : co + d0, 0, 0);
+      }
+    }
+    rscale = 0.f;
+    if (tid < 2 * BKV) {
+      int co, so;
+      key_offsets(tid & (BKV - 1), co, so);
+      rscale = tid < BKV ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsk, so, 0, 0))
+                         : __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsv, so, 0, 0));
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    uint8_t* sk = lds + buf * STAGE;
+    uint8_t* sv = sk + K_TILE;
+    float* ss = reinterpret_cast<float*>(sv + V_TILE);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;
+      const uint2 a = decode4_bf16(rk_code[i][0]);
+      const uint2 b = decode4_bf16(rk_code[i][1]);
+      const uint2 e = decode4_bf16(rk_code[i][2]);
+      const uint2 f = decode4_bf16(rk_code[i][3]);
+      uint4* dst = reinterpret_cast<uint4*>(sk + (c >> 3) * KP + (c & 7) * 32);
+      dst[0] = make_uint4(a.x, a.y, b.x, b.y);
+      dst[1] = make_uint4(e.x, e.y, f.x, f.y);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int task = tid + 256 * i;
+      const int kg = task >> 5, d0 = (task & 31) * 4;
+      // position of key group kg in the permuted order (swap of key bits 2, 3)
+      const int pos = (kg & ~3) * 4 + ((kg & 1) << 3) + ((kg & 2) << 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // byte j of the four key dwords = the codes of d0 + j for keys 4kg..4kg+3
+        const uint32_t lo = __builtin_amdgcn_perm(rv_code[i][1], rv_code[i][0], 0x0c0c0400u + 0x00000101u * j);
+        const uint32_t hi = __builtin_amdgcn_perm(rv_code[i][3], rv_code[i][2], 0x0c0c0400u + 0x00000101u * j);
+        const uint2 dec = decode4_bf16(lo | (hi << 16));
+        *reinterpret_cast<uint2*>(sv + (d0 + j) * VP + pos * 2) = dec;
+      }
+    }
+    if (tid < 2 * BKV) ss[tid] = tid < BKV ? rscale * p.qk_scale : rscale;
+  };
+
+  // ---- Q^T fragments for this wave's 32 queries (kept for the whole kernel)
+  v8bf qf[8];
+  {
+    const int q = q0 + wave * 32 + l32;
+    const bool ok = q < p.Lq;
+    const uint16_t* qp = p.q + static_cast<int64_t>(ok ? q : 0) * p.ldq + h * D + half * 8;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      uint4 v = *reinterpret_cast<const uint4*>(qp + ks * 16);
+      if (!ok) v = make_uint4(0, 0, 0, 0);
+      qf[ks] = __builtin_bit_cast(v8bf, v);
+    }
+  }
+
+  v16f o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  const int n_tiles = (p.n_kv + BKV - 1) / BKV;
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < n_tiles; ++it) {
+    const int cur = it & 1;
+    if (it + 1 < n_tiles) load_tile((it + 1) * BKV);
+    const uint8_t* sk = lds + cur * STAGE;
+    const uint8_t* sv = sk + K_TILE;
+    const float* ss = reinterpret_cast<const float*>(sv + V_TILE);
+
+    // S^T = K Q^T for 2 blocks of 32 keys
+    v16f s[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      s[b] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+      const uint8_t* kr = sk + (b * 32 + l32) * KP + half * 16;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const v8bf kf = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(kr + ks * 32));
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
+      }
+    }
+    // row (key) scaling by c * s_k, masking of keys past n_kv, tile max
+    const int key_base = it * BKV;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int kk = b * 32 + g * 8 + half * 4;
+        const float4 sc = *reinterpret_cast<const float4*>(ss + kk);
+        const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = s[b][4 * g + e] * scv[e];
+          if (key_base + kk + e >= p.n_kv) v = -INFINITY;
+          s[b][4 * g + e] = v;
+          mt = fmaxf(mt, v);
+        }
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    float lsum = 0.f;
+    v8bf pf[4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        uint32_t pk[4];
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2) {
+          const int g = hh * 2 + g2;
+          const int kk = b * 32 + g * 8 + half * 4;
+          const float4 sv4 = *reinterpret_cast<const float4*>(ss + BKV + kk);
+          const float svv[4] = {sv4.x, sv4.y, sv4.z, sv4.w};
+          float pv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float pe = __builtin_amdgcn_exp2f(s[b][4 * g + e] - m_use);
+            lsum += pe;
+            pv[e] = pe * svv[e];
+          }
+          pk[2 * g2] = pack_bf16x2(pv[0], pv[1]);
+          pk[2 * g2 + 1] = pack_bf16x2(pv[2], pv[3]);
+        }
+        pf[b * 2 + hh] = __builtin_bit_cast(v8bf, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+      }
+    }
+    l_run = l_run * alpha + lsum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] *= alpha;
+
+    // O^T += V^T P^T : 4 blocks of 32 d, 4 steps of 16 keys
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint8_t* vr = sv + (db * 32 + l32) * VP + half * 16;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const v8bf vf = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(vr + t * 32));
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t], o[db], 0, 0, 0);
+      }
+    }
+    if (it + 1 < n_tiles) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // normalize and store: lane's query q, d = 32*db + 8*(r/4) + 4*half + r%4
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  const int q = q0 + wave * 32 + l32;
+  if (q < p.Lq) {
+    uint16_t* op = p.out + static_cast<int64_t>(q) * p.ldo + h * D + half * 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint2 w = make_uint2(pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
+                                   pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv));
+        *reinterpret_cast<uint2*>(op + db * 32 + g * 8) = w;
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace wf
+
+extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int32_t head_dim, int64_t ldq,
+                                 const uint8_t* k_codes, const uint8_t* v_codes, const float* k_scales,
+                                 const float* v_scales, int64_t pool_pages, int32_t page_tokens,
+                                 const int32_t* page_table, int64_t n_table, int64_t n_kv, float softmax_scale,
+                                 void* out, int64_t ldo, void* stream) {
+  static const char* fn = "wf_attn_paged_fp8";
+  WF_REQUIRE(lq >= 0 && n_heads > 0 && n_kv >= 0 && page_tokens > 0 && n_table >= 0 && pool_pages >= 0,
+             WF_E_INVALID, "%s: negative or zero size", fn);
+  WF_REQUIRE(head_dim == wf::D, WF_E_SHAPE, "%s: head_dim=%d unsupported (must be 128)", fn, head_dim);
+  WF_REQUIRE(ldq >= static_cast<int64_t>(n_heads) * head_dim && ldo >= static_cast<int64_t>(n_heads) * head_dim,
+             WF_E_INVALID, "%s: ldq/ldo smaller than n_heads*head_dim", fn);
+  if (lq == 0) return WF_OK;
+  WF_REQUIRE(q && out, WF_E_INVALID, "%s: null q/out", fn);
+  WF_REQUIRE(n_kv == 0 || (k_codes && v_codes && k_scales && v_scales && page_table), WF_E_INVALID,
+             "%s: null KV pool or page table", fn);
+  WF_REQUIRE(page_tokens >= wf::BKV, WF_E_SHAPE, "%s: page_tokens=%d must be >= %d", fn, page_tokens, wf::BKV);
+  WF_REQUIRE(n_table * page_tokens >= n_kv, WF_E_SHAPE, "%s: page table covers %lld keys < n_kv=%lld", fn,
+             (long long)(n_table * page_tokens), (long long)n_kv);
+  WF_REQUIRE(pool_pages * page_tokens * n_heads * head_dim < (1ll << 31) - 16, WF_E_SHAPE,
+             "%s: a code pool of 2 GiB or more is not supported", fn);
+  WF_REQUIRE(n_kv < (1ll << 31) && lq < (1ll << 31) && n_table < (1ll << 31), WF_E_SHAPE, "%s: size too large", fn);
+  WF_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15u) == 0 && (ldq % 8) == 0 &&
+                 (reinterpret_cast<uintptr_t>(out) & 7u) == 0 && (ldo % 4) == 0,
+             WF_E_ALIGN, "%s: q must be 16-byte aligned (ldq %% 8 == 0), out 8-byte aligned (ldo %% 4 == 0)", fn);
+  wf::AttnArgs p;
+  p.q = static_cast<const uint16_t*>(q);
+  p.ldq = ldq;
+  p.k_codes = k_codes;
+  p.v_codes = v_codes;
+  p.k_scales = k_scales;
+  p.v_scales = v_scales;
+  p.table = page_table;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  p.Lq = static_cast<int>(lq);
+  p.H = n_heads;
+  p.n_kv = static_cast<int>(n_kv);
+  p.n_table = static_cast<int>(n_table);
+  p.page_tokens = page_tokens;
+  p.pool_pages = static_cast<int>(pool_pages);
+  p.page_div = wf::FastDiv(static_cast<uint32_t>(page_tokens));
+  p.qk_scale = softmax_scale * wf::kLog2e;
+  const dim3 grid(static_cast<uint32_t>((lq + wf::BQ - 1) / wf::BQ), static_cast<uint32_t>(n_heads));
+  hipLaunchKernelGGL(wf::attn_paged_fp8_kernel, grid, dim3(256), 0, wf::as_stream(stream), p);
+  return wf::check_launch(fn);
+}
