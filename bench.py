@@ -37,6 +37,7 @@ from waveforcing_amd.kv import Fp8PagePool  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 LAYERS, TOKENS, HEADS, HEAD_DIM, PAGE = 30, 4680, 12, 128, 1560
 
 
@@ -128,6 +129,29 @@ def bench_gemm(steps: int, warmup: int, dev: str):
             "tops_gemm": ops / (ms_gemm * 1e-3) / 1e12, "tops_linear": ops / (ms_lin * 1e-3) / 1e12}
 
 
+def bench_attention(steps: int, warmup: int, dev: str):
+    """Paged FP8 attention: Q [4680, 12, 128] over 8 chunks (37440 keys) of FP8 pages."""
+    from waveforcing_amd.backend import attn_paged_fp8
+    from waveforcing_amd.kv import PagedKV
+
+    H, chunks = HEADS, 8
+    n_kv = TOKENS * chunks
+    pages = n_kv // PAGE
+    pool = Fp8PagePool(2 * pages, H, HEAD_DIM, PAGE, dev)
+    table = pool.page_table(inputs.page_table(pages, 2 * pages, seed=11))
+    g = torch.Generator().manual_seed(12)
+    k = torch.randn((n_kv, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn((n_kv, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    pool.pack(k, v, table)
+    del k, v
+    q = torch.randn((TOKENS, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    ctx = PagedKV(pool, table, n_kv)
+    out = torch.empty_like(q)
+    ms = _timed(lambda: attn_paged_fp8(q, ctx, out=out), steps, warmup)
+    flops = 4.0 * TOKENS * n_kv * H * HEAD_DIM
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+
+
 def cpu_baseline_kv() -> dict:
     """Oracle torch-CPU pack (quantize + page scatter) of a bounded sample of layers."""
     from oracle import kv as okv
@@ -182,6 +206,7 @@ def main() -> None:
     dev = "cuda:0"
     kv = bench_kv(args.steps, args.warmup, dev)
     gm = bench_gemm(args.steps, args.warmup, dev)
+    at = bench_attention(args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     # one launch per step: the launch duration is the step time
     achieved = kv["bytes_per_step"] / (kv["ms_pack"] * 1e-3) / 1e9
@@ -226,6 +251,10 @@ def main() -> None:
             "w8a8_linear_tops_incl_act_quant": round(gm["tops_linear"], 1),
             "w8a8_linear_us_incl_act_quant": round(gm["ms_linear"] * 1e3, 2),
             "w8a8_shape": "x[4680,1536] . W[1536,1536]^T int8, per-token/per-channel scales, bias, bf16 out",
+            "attn_paged_fp8_ms": round(at["ms"], 4),
+            "attn_paged_fp8_roofline": {"bound": "mfma", "achieved": round(at["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
+                                        "unit": "TFLOP/s", "frac": round(at["tflops"] / BF16_PEAK_TFLOPS, 4)},
+            "attn_shape": "Q[4680,12,128] bf16 over 37440 keys (8 chunks) of FP8 e4m3fn pages, bf16 MFMA",
         },
     }
     print(json.dumps(line), flush=True)

@@ -11,8 +11,8 @@
 // naive_rt/rolling_forcing/wan/modules/attention.py:75-89) on the FP8 pages
 // that replace the bf16 slab views of paged.py:246-247.
 //
-// Work split: a workgroup of 4 waves owns 128 queries of one head; each wave
-// owns 32 queries.  Keys advance in tiles of 64.  Per tile the workgroup
+// Work split: a workgroup of WAVES waves owns 32 * WAVES queries of one
+// head; each wave owns 32 queries.  Keys advance in tiles of 64.  Per tile the workgroup
 // loads the K and V codes of the tile (through buffer descriptors over the
 // pools: keys past n_kv or on invalid pages read as zero) and the per-key
 // scales, decodes the codes once to bf16 (exact) into LDS, K as [key][d] and
@@ -42,7 +42,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int D = 128;
-constexpr int BQ = 128;          // queries per workgroup (4 waves x 32)
 constexpr int BKV = 64;          // keys per tile
 constexpr int KP = D * 2 + 16;   // K tile row pitch (bytes, bf16 + pad) = 272
 constexpr int VP = BKV * 2 + 16; // V^T tile row pitch (bytes) = 144
@@ -69,9 +68,22 @@ struct AttnArgs {
   float qk_scale;  // softmax scale * log2(e)
 };
 
+// XOR swizzle (in key positions, a multiple of 8 = one 16-byte fragment) of
+// V^T row d: the transposing writes of lanes holding d, d+4, d+8, ... would
+// otherwise all hit 4 bank groups; fragments stay contiguous 16-byte reads.
+__device__ inline int vswz(int d) { return ((d >> 4) & 7) * 8; }
+
 // Two fp32 holding e4m3-exact values -> packed bf16x2 (truncation is exact).
 __device__ inline uint32_t f32x2_to_bf16x2_exact(float lo, float hi) {
   return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
+}
+
+// Two fp32 -> packed bf16x2, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ inline uint32_t cvt_bf16x2(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const f2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
 }
 
 // Decode 4 e4m3 codes (bytes of w) into 2 dwords of packed bf16.
@@ -81,7 +93,23 @@ __device__ inline uint2 decode4_bf16(uint32_t w) {
   return make_uint2(f32x2_to_bf16x2_exact(a, b), f32x2_to_bf16x2_exact(c, d));
 }
 
-__global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
+template <int N, typename F, int... I>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+// WAVES waves of 32 queries each share one decoded K/V tile; PGR register
+// buffers let the loads of tile it + PGR fly while tile it computes.
+template <int WAVES, int PGR>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(AttnArgs p) {
+  constexpr int THREADS = WAVES * 64;
+  constexpr int BQ = WAVES * 32;
+  constexpr int KCH = BKV * 8 / THREADS;  // 16-code K chunks per thread per tile
+  constexpr int VT = BKV * D / 16 / THREADS;  // 4-key x 4-d V tasks per thread per tile
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
 
   const int tid = threadIdx.x;
@@ -89,8 +117,17 @@ __global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
   const int wave = tid >> 6;
   const int l32 = lane & 31;
   const int half = lane >> 5;
-  const int h = blockIdx.y;
-  const int q0 = blockIdx.x * BQ;
+  // Work item w = head * q_tiles + q_tile.  Workgroups are dealt to the 8
+  // XCDs round-robin (blockIdx % 8); each XCD gets a contiguous range of
+  // work items, so the query tiles of one head share that head's K/V tiles
+  // in one L2.
+  const int q_tiles = (p.Lq + BQ - 1) / BQ;
+  const int n_items = q_tiles * p.H;
+  const int per_xcd = (n_items + 7) / 8;
+  const int w_item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (w_item >= n_items) return;
+  const int h = w_item / q_tiles;
+  const int q0 = (w_item % q_tiles) * BQ;
 
   const int64_t pool_bytes = static_cast<int64_t>(p.pool_pages) * p.page_tokens * p.H * D;
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.k_codes), 0,
@@ -135,70 +172,69 @@ __global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
   // V: 2 tasks of 4 keys x 4 d (dword loads), task = tid + 256 * i:
   //    key group kg = task / 32 (keys 4kg..4kg+3), d = 4 * (task % 32).
   // Scales: threads 0..63 load s_k of key tid, 64..127 s_v of key tid - 64.
-  u32x4 rk_code[2];
-  uint32_t rv_code[2][4];
-  float rscale;
+  u32x4 rk_code[PGR][KCH];
+  uint32_t rv_code[PGR][VT][4];
+  float rscale[PGR];
 
-  auto load_tile = [&](int t0) {
+  auto load_tile = [&](auto buf, int t0) {
+    constexpr int u = decltype(buf)::value;
     map_tile(t0);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i;
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + THREADS * i;
       int co, so;
       key_offsets(c >> 3, co, so);
-      rk_code[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, co == kOutOfRange ? co : co + (c & 7) * 16, 0, 0);
+      rk_code[u][i] = __builtin_amdgcn_raw_buffer_load_b128(rk, co == kOutOfRange ? co : co + (c & 7) * 16, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int task = tid + 256 * i;
+    for (int i = 0; i < VT; ++i) {
+      const int task = tid + THREADS * i;
       const int kg = task >> 5, d0 = (task & 31) * 4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         int co, so;
         key_offsets(4 * kg + j, co, so);
-        rv_code[i][j] = __builtin_amdgcn_raw_buffer_load_b32(rv, co == kOutOfRange ? co : co + d0, 0, 0);
+        rv_code[u][i][j] = __builtin_amdgcn_raw_buffer_load_b32(rv, co == kOutOfRange ? co : co + d0, 0, 0);
       }
     }
-    rscale = 0.f;
-    if (tid < 2 * BKV) {
-      int co, so;
-      key_offsets(tid & (BKV - 1), co, so);
-      rscale = tid < BKV ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsk, so, 0, 0))
-                         : __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsv, so, 0, 0));
-    }
+    // threads 0..63 fetch s_k, 64..127 s_v (others fetch a dummy s_v)
+    int co, so;
+    key_offsets(tid & (BKV - 1), co, so);
+    rscale[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tid < BKV ? rsk : rsv, so, 0, 0));
   };
 
-  auto store_tile = [&](int buf) {
-    uint8_t* sk = lds + buf * STAGE;
+  auto store_tile = [&](auto buf, int lbuf) {
+    constexpr int u = decltype(buf)::value;
+    uint8_t* sk = lds + lbuf * STAGE;
     uint8_t* sv = sk + K_TILE;
     float* ss = reinterpret_cast<float*>(sv + V_TILE);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i;
-      const uint2 a = decode4_bf16(rk_code[i][0]);
-      const uint2 b = decode4_bf16(rk_code[i][1]);
-      const uint2 e = decode4_bf16(rk_code[i][2]);
-      const uint2 f = decode4_bf16(rk_code[i][3]);
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + THREADS * i;
+      const uint2 a = decode4_bf16(rk_code[u][i][0]);
+      const uint2 b = decode4_bf16(rk_code[u][i][1]);
+      const uint2 e = decode4_bf16(rk_code[u][i][2]);
+      const uint2 f = decode4_bf16(rk_code[u][i][3]);
       uint4* dst = reinterpret_cast<uint4*>(sk + (c >> 3) * KP + (c & 7) * 32);
       dst[0] = make_uint4(a.x, a.y, b.x, b.y);
       dst[1] = make_uint4(e.x, e.y, f.x, f.y);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int task = tid + 256 * i;
+    for (int i = 0; i < VT; ++i) {
+      const int task = tid + THREADS * i;
       const int kg = task >> 5, d0 = (task & 31) * 4;
       // position of key group kg in the permuted order (swap of key bits 2, 3)
-      const int pos = (kg & ~3) * 4 + ((kg & 1) << 3) + ((kg & 2) << 1);
+      const int pos = ((kg & ~3) * 4 + ((kg & 1) << 3) + ((kg & 2) << 1)) ^ vswz(d0);  // d0..d0+3 share vswz
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         // byte j of the four key dwords = the codes of d0 + j for keys 4kg..4kg+3
-        const uint32_t lo = __builtin_amdgcn_perm(rv_code[i][1], rv_code[i][0], 0x0c0c0400u + 0x00000101u * j);
-        const uint32_t hi = __builtin_amdgcn_perm(rv_code[i][3], rv_code[i][2], 0x0c0c0400u + 0x00000101u * j);
+        const uint32_t lo = __builtin_amdgcn_perm(rv_code[u][i][1], rv_code[u][i][0], 0x0c0c0400u + 0x00000101u * j);
+        const uint32_t hi = __builtin_amdgcn_perm(rv_code[u][i][3], rv_code[u][i][2], 0x0c0c0400u + 0x00000101u * j);
         const uint2 dec = decode4_bf16(lo | (hi << 16));
         *reinterpret_cast<uint2*>(sv + (d0 + j) * VP + pos * 2) = dec;
       }
     }
-    if (tid < 2 * BKV) ss[tid] = tid < BKV ? rscale * p.qk_scale : rscale;
+    if (tid < 2 * BKV) ss[tid] = tid < BKV ? rscale[u] * p.qk_scale : rscale[u];
   };
 
   // ---- Q^T fragments for this wave's 32 queries (kept for the whole kernel)
@@ -222,15 +258,20 @@ __global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
   float l_run = 0.f;
 
   const int n_tiles = (p.n_kv + BKV - 1) / BKV;
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  // Tiles past the context read as zero (all keys masked by n_kv), so the
+  // step count is padded to a multiple of PGR and every step is
+  // unconditional.
+  const int n_steps = (n_tiles + PGR - 1) / PGR * PGR;
+  static_for<PGR>([&](auto u) { load_tile(u, u.value * BKV); });
+  store_tile(std::integral_constant<int, 0>{}, 0);
   __syncthreads();
 
-  for (int it = 0; it < n_tiles; ++it) {
+  for (int it0 = 0; it0 < n_steps; it0 += PGR) {
+  static_for<PGR>([&](auto uu) {
+    constexpr int U = decltype(uu)::value;
+    const int it = it0 + U;
     const int cur = it & 1;
-    if (it + 1 < n_tiles) load_tile((it + 1) * BKV);
+    load_tile(uu, (it + PGR) * BKV);
     const uint8_t* sk = lds + cur * STAGE;
     const uint8_t* sv = sk + K_TILE;
     const float* ss = reinterpret_cast<const float*>(sv + V_TILE);
@@ -249,6 +290,7 @@ __global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
     }
     // row (key) scaling by c * s_k, masking of keys past n_kv, tile max
     const int key_base = it * BKV;
+    const bool partial = key_base + BKV > p.n_kv;
     float mt = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -260,7 +302,7 @@ __global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float v = s[b][4 * g + e] * scv[e];
-          if (key_base + kk + e >= p.n_kv) v = -INFINITY;
+          if (partial && key_base + kk + e >= p.n_kv) v = -INFINITY;
           s[b][4 * g + e] = v;
           mt = fmaxf(mt, v);
         }
@@ -291,28 +333,33 @@ __global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
             lsum += pe;
             pv[e] = pe * svv[e];
           }
-          pk[2 * g2] = pack_bf16x2(pv[0], pv[1]);
-          pk[2 * g2 + 1] = pack_bf16x2(pv[2], pv[3]);
+          pk[2 * g2] = cvt_bf16x2(pv[0], pv[1]);
+          pk[2 * g2 + 1] = cvt_bf16x2(pv[2], pv[3]);
         }
         pf[b * 2 + hh] = __builtin_bit_cast(v8bf, make_uint4(pk[0], pk[1], pk[2], pk[3]));
       }
     }
     l_run = l_run * alpha + lsum;
+    if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] *= alpha;
+      for (int i = 0; i < 4; ++i) o[i] *= alpha;
+    }
 
     // O^T += V^T P^T : 4 blocks of 32 d, 4 steps of 16 keys
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const uint8_t* vr = sv + (db * 32 + l32) * VP + half * 16;
+      const int d = db * 32 + l32;
+      const uint8_t* vr = sv + d * VP;
+      const int sw = vswz(d);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const v8bf vf = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(vr + t * 32));
+        const v8bf vf = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(vr + (((t * 16 + half * 8) ^ sw) * 2)));
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t], o[db], 0, 0, 0);
       }
     }
-    if (it + 1 < n_tiles) store_tile(cur ^ 1);
+    store_tile(std::integral_constant<int, (U + 1) % PGR>{}, cur ^ 1);
     __syncthreads();
+  });
   }
 
   // normalize and store: lane's query q, d = 32*db + 8*(r/4) + 4*half + r%4
@@ -325,8 +372,8 @@ __global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const uint2 w = make_uint2(pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
-                                   pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv));
+        const uint2 w = make_uint2(cvt_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
+                                   cvt_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv));
         *reinterpret_cast<uint2*>(op + db * 32 + g * 8) = w;
       }
     }
@@ -334,6 +381,15 @@ __global__ __launch_bounds__(256, 2) void attn_paged_fp8_kernel(AttnArgs p) {
 }
 
 }  // namespace
+
+template <int WAVES, int PGR>
+int launch_attn(const AttnArgs& p, int64_t lq, int n_heads, hipStream_t stream) {
+  const int64_t items = (lq + WAVES * 32 - 1) / (WAVES * 32) * n_heads;
+  const dim3 grid(static_cast<uint32_t>((items + 7) / 8 * 8));
+  hipLaunchKernelGGL((attn_paged_fp8_kernel<WAVES, PGR>), grid, dim3(WAVES * 64), 0, stream, p);
+  return check_launch("wf_attn_paged_fp8");
+}
+
 }  // namespace wf
 
 extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int32_t head_dim, int64_t ldq,
@@ -378,7 +434,8 @@ extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int
   p.pool_pages = static_cast<int>(pool_pages);
   p.page_div = wf::FastDiv(static_cast<uint32_t>(page_tokens));
   p.qk_scale = softmax_scale * wf::kLog2e;
-  const dim3 grid(static_cast<uint32_t>((lq + wf::BQ - 1) / wf::BQ), static_cast<uint32_t>(n_heads));
-  hipLaunchKernelGGL(wf::attn_paged_fp8_kernel, grid, dim3(256), 0, wf::as_stream(stream), p);
-  return wf::check_launch(fn);
+  // 8 waves (256 queries) share each decoded K/V tile, one tile of register
+  // prefetch: the best of {4, 8} waves x {1, 2} tiles of prefetch measured on
+  // the 1.3B / 14B context shapes.
+  return wf::launch_attn<8, 1>(p, lq, n_heads, wf::as_stream(stream));
 }
