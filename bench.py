@@ -152,6 +152,41 @@ def bench_attention(steps: int, warmup: int, dev: str):
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
 
 
+def bench_block(scale: str, steps: int, warmup: int, dev: str):
+    """One quantized DiT block over one 3-frame chunk (4680 tokens, 30x52 latent grid) with 7 prior
+    chunks of FP8 paged context (37440 keys incl. its own) and a 512-token text context."""
+    from waveforcing_amd import rope
+    from waveforcing_amd.block import PRESETS, QuantizedWanBlock, random_block_params
+
+    cfg = PRESETS[scale]
+    dim, heads, ffn = cfg["dim"], cfg["heads"], cfg["ffn_dim"]
+    frames, h, w = 3, 30, 52
+    T = frames * h * w
+    prior = 7
+    pages = (prior + 1) * frames
+    blk = QuantizedWanBlock(random_block_params(dim, ffn, seed=3), heads, dev)
+    pool = Fp8PagePool(pages, heads, HEAD_DIM, PAGE, dev)
+    g = torch.Generator().manual_seed(4)
+    prior_kv = torch.randn((prior * T, heads, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    pool.pack(prior_kv, prior_kv, pool.page_table(list(range(prior * frames))))
+    del prior_kv
+    ctx = pool.page_table(list(range(pages)))
+    own = pool.page_table(list(range(prior * frames, pages)))
+    text = torch.randn((512, dim), generator=g).to(torch.bfloat16).to(dev)
+    tkv = blk.text_kv(text)
+    cos, sin = rope.cos_sin(frames, h, w, prior * frames, device=dev)
+    x0 = torch.randn((T, dim), generator=g).to(torch.bfloat16).to(dev)
+    e = (torch.randn((frames, 6, dim), generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    x = x0.clone()
+
+    def step():
+        x.copy_(x0)
+        blk.forward(x, e, cos, sin, pool, ctx, own, (prior + 1) * T, tkv)
+
+    ms = _timed(step, steps, warmup)
+    return {"ms": ms, "tokens": T, "context_keys": (prior + 1) * T}
+
+
 def cpu_baseline_kv() -> dict:
     """Oracle torch-CPU pack (quantize + page scatter) of a bounded sample of layers."""
     from oracle import kv as okv
@@ -207,6 +242,8 @@ def main() -> None:
     kv = bench_kv(args.steps, args.warmup, dev)
     gm = bench_gemm(args.steps, args.warmup, dev)
     at = bench_attention(args.steps, args.warmup, dev)
+    b13 = bench_block("1.3b", args.steps, args.warmup, dev)
+    b14 = bench_block("14b", max(3, args.steps // 4), 1, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     # one launch per step: the launch duration is the step time
     achieved = kv["bytes_per_step"] / (kv["ms_pack"] * 1e-3) / 1e9
@@ -255,6 +292,11 @@ def main() -> None:
             "attn_paged_fp8_roofline": {"bound": "mfma", "achieved": round(at["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
                                         "unit": "TFLOP/s", "frac": round(at["tflops"] / BF16_PEAK_TFLOPS, 4)},
             "attn_shape": "Q[4680,12,128] bf16 over 37440 keys (8 chunks) of FP8 e4m3fn pages, bf16 MFMA",
+            "dit_block_1p3b_ms_per_chunk": round(b13["ms"], 4),
+            "dit_block_14b_ms_per_chunk": round(b14["ms"], 4),
+            "dit_block_note": "one block, 4680-token 3-frame chunk, 37440-key FP8 paged self-attn context, "
+                              "512-token text cross-attn, all linears W8A8 int8, random init; includes a 9.4/31 MB "
+                              "copy to reset x each step",
         },
     }
     print(json.dumps(line), flush=True)

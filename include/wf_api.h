@@ -72,14 +72,15 @@ int wf_fp8_e4m3_decode_f32(const uint8_t* codes, float* out, int64_t n,
  * per (token, head) in place of per tensor.
  */
 
-/* Pack bf16 K and V [n_tokens][n_heads][head_dim] into the pools.
+/* Pack bf16 K and V [n_tokens][n_heads][head_dim] (token stride ld_kv
+ * elements, >= n_heads * head_dim, % 8 == 0) into the pools.
  * `v` / `v_codes` / `v_scales` may all be NULL to pack K only.
  * head_dim must be 128.  Replaces the quantize half of
  * _all_gather_fp8 (wave_rt/denoiser/exchange/common.py:143-150) and the
  * slot copies of _publish_paged (wave_rt/denoiser/exchange/paged.py:120-141)
  * on a single GPU. */
 int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens,
-                   int32_t n_heads, int32_t head_dim,
+                   int32_t n_heads, int32_t head_dim, int64_t ld_kv,
                    const int32_t* page_table, int64_t n_table,
                    int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes,
                    float* k_scales, float* v_scales, int64_t pool_pages,
@@ -159,6 +160,51 @@ int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads,
                       int32_t page_tokens, const int32_t* page_table,
                       int64_t n_table, int64_t n_kv, float softmax_scale,
                       void* out, int64_t ldo, void* stream);
+
+/* Attention of q [lq][n_heads][128] over dense bf16 K, V [n_kv][n_heads][128]
+ * (token stride ldkv elements), same math and output as wf_attn_paged_fp8
+ * with unit scales.  Replaces the text cross-attention's flash_attention
+ * call (naive_rt/rolling_forcing/wan/modules/model.py:189, the SDPA
+ * fallback attention.py:75-89) over the cached 512-token text K/V. */
+int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads,
+                       int32_t head_dim, int64_t ldq, const void* k,
+                       const void* v, int64_t n_kv, int64_t ldkv,
+                       float softmax_scale, void* out, int64_t ldo,
+                       void* stream);
+
+/* ------------------------------------------------- block row-wise stages */
+
+/* y = LayerNorm(x) (fp32 statistics, optional bf16 affine w/b, rounded to
+ * bf16), then, if given, the bf16 modulation y = bf16(bf16(y * bf16(1 +
+ * scale[f])) + shift[f]) with f = row / frame_tokens (scale/shift bf16
+ * [frames][dim]); writes y (bf16, row stride ldo) if out != NULL and its
+ * per-token int8 quantization (as wf_quant_rows_i8) if q != NULL.
+ * dim % 8 == 0, dim <= 5120.  Replaces norm1/norm2 + modulation
+ * (naive_rt/rolling_forcing/wan/modules/causal_model.py:381,393-394) and
+ * norm3 (:390, model.py:89-99) feeding the W8A8 linears. */
+int wf_ln_modulate_quant(const void* x, int64_t T, int32_t dim, int64_t ldx,
+                         float eps, const void* w, const void* b,
+                         const void* shift, const void* scale,
+                         int32_t frame_tokens, void* out, int64_t ldo,
+                         int8_t* q, float* q_scales, void* stream);
+
+/* y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w) over the full row (dim),
+ * then, if cos/sin ([T][head_dim/2] fp32) are given, each head's
+ * interleaved pairs (y[2i], y[2i+1]) are rotated by angle i of the row.
+ * Replaces norm_q/norm_k (causal_model.py:112-116, model.py:70-86) and the
+ * RoPE of the patched forward (wave_rt/runtime/backend.py:119-121). */
+int wf_rmsnorm_rope(const void* x, int64_t T, int32_t dim, int64_t ldx,
+                    int32_t head_dim, float eps, const void* w,
+                    const float* cos, const float* sin, void* out,
+                    int64_t ldo, void* stream);
+
+/* In place x = bf16(x + bf16(y * gate[row / frame_tokens])), or
+ * x = bf16(x + y) when gate is NULL (gate bf16 [frames][dim]).  The gated
+ * residuals of causal_model.py:386,397-398 and the cross-attention residual
+ * of :390. */
+int wf_gate_residual(void* x, int64_t ldx, const void* y, int64_t ldy,
+                     const void* gate, int64_t T, int32_t dim,
+                     int32_t frame_tokens, void* stream);
 
 #ifdef __cplusplus
 }

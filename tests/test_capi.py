@@ -33,12 +33,12 @@ def test_abi_version():
 
 def test_bad_head_dim_is_rejected():
     with pytest.raises(RuntimeError, match="head_dim=64"):
-        _lib.call("wf_fp8_kv_pack", 1, 2, 10, 2, 64, 3, 1, 16, 4, 5, 6, 7, 4, None)
+        _lib.call("wf_fp8_kv_pack", 1, 2, 10, 2, 64, 128, 3, 1, 16, 4, 5, 6, 7, 4, None)
 
 
 def test_short_page_table_is_rejected():
     with pytest.raises(RuntimeError, match="page table covers"):
-        _lib.call("wf_fp8_kv_pack", 16, 32, 100, 2, 128, 48, 1, 16, 64, 80, 96, 112, 4, None)
+        _lib.call("wf_fp8_kv_pack", 16, 32, 100, 2, 128, 256, 48, 1, 16, 64, 80, 96, 112, 4, None)
 
 
 def test_negative_size_is_rejected():
@@ -48,7 +48,7 @@ def test_negative_size_is_rejected():
 
 def test_unaligned_pointer_is_rejected():
     with pytest.raises(RuntimeError, match="16-byte aligned"):
-        _lib.call("wf_fp8_kv_pack", 17, 32, 10, 2, 128, 48, 1, 16, 64, 80, 96, 112, 4, None)
+        _lib.call("wf_fp8_kv_pack", 17, 32, 10, 2, 128, 256, 48, 1, 16, 64, 80, 96, 112, 4, None)
 
 
 def test_last_error_is_thread_local_text():

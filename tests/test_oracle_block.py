@@ -1,0 +1,62 @@
+"""Pins the block oracle (oracle/block.py) on the CPU.
+
+- zero linear weights and biases leave x unchanged (every branch is a
+  residual; no stray term);
+- RoPE: position (0, 0, 0) of a chunk starting at frame 0 is the identity,
+  rotations preserve each pair's norm, and the angle table equals the host
+  table generator's (waveforcing_amd.rope, written separately);
+- the norms match torch's layer_norm / the closed-form RMS definition in
+  float64.
+"""
+
+import dataclasses
+
+import torch
+
+from oracle import block as ob
+from oracle import kv as okv
+from waveforcing_amd import rope
+from waveforcing_amd.block import random_block_params
+
+
+def test_zero_weights_identity():
+    dim, heads, ffn = 256, 2, 512
+    p = random_block_params(dim, ffn, seed=1)
+    zero = {f.name: torch.zeros_like(getattr(p, f.name)) for f in dataclasses.fields(p)
+            if f.name.endswith(("_w", "_b")) and not f.name.startswith("norm3")}
+    p = dataclasses.replace(p, **zero)
+    frames, h, w = 3, 8, 8
+    T = frames * h * w
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn((T, dim), generator=g).to(torch.bfloat16)
+    e = (torch.randn((frames, 6, dim), generator=g) * 0.1).to(torch.bfloat16)
+    pk = okv.new_pool(3, 64, heads, 128)
+    pv = okv.new_pool(3, 64, heads, 128)
+    tk = torch.zeros((16, heads, 128), dtype=torch.bfloat16)
+    out = ob.block_forward(p, x, e, (frames, h, w), 0, pk, pv, [0, 1, 2], [0, 1, 2], T, 64, tk, tk, heads)
+    assert torch.equal(out, x)
+
+
+def test_rope_identity_norm_and_table():
+    ang = ob.rope_angles(3, 4, 5, 0)
+    assert torch.equal(ang[0], torch.zeros(64, dtype=torch.float64))
+    assert torch.allclose(ang, rope.angles(3, 4, 5, 0), rtol=0, atol=0)
+    assert torch.allclose(ob.rope_angles(3, 4, 5, 7), rope.angles(3, 4, 5, 7), rtol=0, atol=0)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((60, 2, 128), generator=g).to(torch.bfloat16)
+    y = ob.rope_apply(x, ob.rope_angles(3, 4, 5, 2))
+    assert torch.equal(ob.rope_apply(x[:1], torch.zeros((1, 64), dtype=torch.float64)), x[:1])
+    nx = x.double().reshape(60, 2, 64, 2).norm(dim=-1)
+    ny = y.double().reshape(60, 2, 64, 2).norm(dim=-1)
+    assert torch.allclose(nx, ny, rtol=2 ** -7, atol=1e-6)
+
+
+def test_norms_match_definitions():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn((32, 384), generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(384, generator=g)).to(torch.bfloat16)
+    xd = x.double()
+    ln = (xd - xd.mean(-1, keepdim=True)) / torch.sqrt(xd.var(-1, unbiased=False, keepdim=True) + 1e-6)
+    assert torch.allclose(ob.layer_norm(x).double(), ln, rtol=2 ** -7, atol=1e-2)
+    rms = xd / torch.sqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6) * w.double()
+    assert torch.allclose(ob.rms_norm(x, w).double(), rms, rtol=2 ** -6, atol=1e-2)

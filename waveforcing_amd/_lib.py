@@ -28,7 +28,7 @@ SIGNATURES: dict[str, list] = {
     "wf_fp8_e4m3_encode_f32": [_c_void_p, _c_void_p, _i64, _c_void_p],
     "wf_fp8_e4m3_decode_f32": [_c_void_p, _c_void_p, _i64, _c_void_p],
     "wf_fp8_kv_pack": [
-        _c_void_p, _c_void_p, _i64, _i32, _i32,
+        _c_void_p, _c_void_p, _i64, _i32, _i32, _i64,
         _c_void_p, _i64, _i32,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
         _c_void_p,
@@ -52,6 +52,17 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _i64, _i32, _c_void_p, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p,
     ],
+    "wf_attn_dense_bf16": [
+        _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p,
+    ],
+    "wf_ln_modulate_quant": [
+        _c_void_p, _i64, _i32, _i64, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32,
+        _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
+    ],
+    "wf_rmsnorm_rope": [
+        _c_void_p, _i64, _i32, _i64, _i32, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
+    ],
+    "wf_gate_residual": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i32, _i32, _c_void_p],
 }
 
 GEMM_GELU_TANH = 1

@@ -88,6 +88,32 @@ def attn_paged_fp8(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, causal
     return o.unsqueeze(0) if squeeze else o
 
 
+def attn_dense_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale: float | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Non-causal attention of q [Lq, H, D] over dense bf16 k, v [Lk, H, D] (text cross-attention)."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dim() != 3 or t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bf16 [L, H, D], got {tuple(t.shape)} {t.dtype}")
+    Lq, H, D = q.shape
+    if k.shape != v.shape or k.shape[1:] != (H, D):
+        raise ValueError("k/v shapes must match and agree with q's heads and head_dim")
+
+    def rows(t):
+        if t.stride(2) != 1 or t.stride(1) != D or t.stride(0) % 8 or t.data_ptr() % 16:
+            t = t.contiguous()
+        return t
+
+    q, k, v = rows(q), rows(k), rows(v)
+    if k.stride(0) != v.stride(0):
+        k, v = k.contiguous(), v.contiguous()
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    o = out if out is not None else torch.empty((Lq, H, D), dtype=torch.bfloat16, device=q.device)
+    _lib.call("wf_attn_dense_bf16", q.data_ptr(), Lq, H, D, q.stride(0), k.data_ptr(), v.data_ptr(), k.shape[0],
+              k.stride(0), float(softmax_scale), o.data_ptr(), o.stride(0), _lib.stream_handle(q.device))
+    return o
+
+
 def enable_hip_fp8() -> None:
     """Use the gfx950 paged-FP8 attention on the wavefront path."""
     _WAVE_STATE["attn"] = "hip_fp8"

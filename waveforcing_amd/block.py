@@ -1,0 +1,254 @@
+"""The Wan attention block on the quantized HIP path, for one chunk on one GPU.
+
+Restates CausalWanAttentionBlock.forward
+(naive_rt/rolling_forcing/wan/modules/causal_model.py:349-402), the block that
+WaveRT's SGLang model runs (F4 of the path's survey), with:
+
+* every block linear W8A8 int8 (the ``scope=all`` swap of
+  wave_rt/runtime/fp8.py:93-137, per-token / per-channel int8);
+* norm + modulation + activation quantization fused into one row kernel;
+* q/k RMSNorm + 3-D RoPE fused into one row kernel;
+* self-attention over the FP8 paged context: this chunk's K/V are packed
+  into its pages, then attention reads the prior chunks' pages plus its own
+  (the single-GPU form of the paged exchange, paged.py:206-247);
+* text cross-attention over the cached 512-token K/V (crossattn_cache,
+  model.py:174-183) in the dense-bf16 variant of the attention kernel;
+* GELU(tanh) fused into the fc_in epilogue; gated residuals in bf16.
+
+Every step is a HIP kernel from libwf_mi355x.so; torch only allocates and
+slices tensors.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, fields
+
+import torch
+
+from . import _lib, rope
+from .backend import attn_dense_bf16, attn_paged_fp8
+from .fp8 import _quant_rows_i8, gemm_i8
+from .kv import Fp8PagePool, PagedKV, PageTable
+
+# Wan2.1 shapes (wave_rt/runtime/dummy_model.py:25-35)
+PRESETS = {
+    "1.3b": dict(dim=1536, heads=12, ffn_dim=8960, layers=30),
+    "14b": dict(dim=5120, heads=40, ffn_dim=13824, layers=40),
+}
+EPS = 1e-6
+
+
+@dataclass
+class BlockParams:
+    """bf16 parameters of one attention block (nn.Linear layout [out, in])."""
+
+    modulation: torch.Tensor  # [1, 6, dim]
+    q_w: torch.Tensor
+    q_b: torch.Tensor
+    k_w: torch.Tensor
+    k_b: torch.Tensor
+    v_w: torch.Tensor
+    v_b: torch.Tensor
+    o_w: torch.Tensor
+    o_b: torch.Tensor
+    norm_q: torch.Tensor
+    norm_k: torch.Tensor
+    norm3_w: torch.Tensor
+    norm3_b: torch.Tensor
+    cq_w: torch.Tensor
+    cq_b: torch.Tensor
+    ck_w: torch.Tensor
+    ck_b: torch.Tensor
+    cv_w: torch.Tensor
+    cv_b: torch.Tensor
+    co_w: torch.Tensor
+    co_b: torch.Tensor
+    cnorm_q: torch.Tensor
+    cnorm_k: torch.Tensor
+    fc_in_w: torch.Tensor
+    fc_in_b: torch.Tensor
+    fc_out_w: torch.Tensor
+    fc_out_b: torch.Tensor
+
+    @property
+    def dim(self) -> int:
+        return self.q_w.shape[0]
+
+    def to(self, device) -> "BlockParams":
+        return BlockParams(**{f.name: getattr(self, f.name).to(device) for f in fields(self)})
+
+
+def random_block_params(dim: int, ffn_dim: int, seed: int = 0, w_std: float = 0.02) -> BlockParams:
+    """Seeded random-init block (CPU, bf16): linears ~ N(0, w_std), biases ~ N(0, 0.01), norm
+    weights ~ 1 + N(0, 0.05), modulation ~ N(0, 1) / sqrt(dim) (causal_model.py:347)."""
+    g = torch.Generator().manual_seed(seed)
+
+    def lin(o, i):
+        return (torch.randn((o, i), generator=g) * w_std).to(torch.bfloat16)
+
+    def vec(n, std=0.01, mean=0.0):
+        return (torch.randn((n,), generator=g) * std + mean).to(torch.bfloat16)
+
+    return BlockParams(
+        modulation=(torch.randn((1, 6, dim), generator=g) / dim ** 0.5).to(torch.bfloat16),
+        q_w=lin(dim, dim), q_b=vec(dim), k_w=lin(dim, dim), k_b=vec(dim), v_w=lin(dim, dim), v_b=vec(dim),
+        o_w=lin(dim, dim), o_b=vec(dim), norm_q=vec(dim, 0.05, 1.0), norm_k=vec(dim, 0.05, 1.0),
+        norm3_w=vec(dim, 0.05, 1.0), norm3_b=vec(dim),
+        cq_w=lin(dim, dim), cq_b=vec(dim), ck_w=lin(dim, dim), ck_b=vec(dim), cv_w=lin(dim, dim), cv_b=vec(dim),
+        co_w=lin(dim, dim), co_b=vec(dim), cnorm_q=vec(dim, 0.05, 1.0), cnorm_k=vec(dim, 0.05, 1.0),
+        fc_in_w=lin(ffn_dim, dim), fc_in_b=vec(ffn_dim), fc_out_w=lin(dim, ffn_dim), fc_out_b=vec(dim),
+    )
+
+
+@dataclass
+class QLinear:
+    """Pre-quantized int8 weight [out, in] with per-channel scales and bf16 bias."""
+
+    w: torch.Tensor
+    s: torch.Tensor
+    b: torch.Tensor | None
+
+    @classmethod
+    def from_bf16(cls, w: torch.Tensor, b: torch.Tensor | None, device) -> "QLinear":
+        qw, sw = _quant_rows_i8(w.to(device).contiguous())
+        return cls(qw, sw, None if b is None else b.to(device).contiguous())
+
+
+def _ln_quant(x, dim, frame_tokens, q, qs, out=None, w=None, b=None, shift=None, scale=None):
+    T = x.shape[0]
+    _lib.call("wf_ln_modulate_quant", x.data_ptr(), T, dim, x.stride(0), EPS, _lib.ptr(w), _lib.ptr(b),
+              _lib.ptr(shift), _lib.ptr(scale), frame_tokens, _lib.ptr(out), out.stride(0) if out is not None else 0,
+              _lib.ptr(q), _lib.ptr(qs), _lib.stream_handle(x.device))
+
+
+def _rmsnorm_rope(x, head_dim, w, cos, sin, out):
+    T, dim = x.shape
+    _lib.call("wf_rmsnorm_rope", x.data_ptr(), T, dim, x.stride(0), head_dim, EPS, w.data_ptr(), _lib.ptr(cos),
+              _lib.ptr(sin), out.data_ptr(), out.stride(0), _lib.stream_handle(x.device))
+
+
+def _gate_residual(x, y, gate, frame_tokens):
+    T, dim = x.shape
+    _lib.call("wf_gate_residual", x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), _lib.ptr(gate), T, dim,
+              frame_tokens, _lib.stream_handle(x.device))
+
+
+def _linear_i8(x, lin: QLinear, ws_q, ws_s, out, gelu=False):
+    """W8A8 linear of bf16 x [M, K] into out [M, N] via the fused C entry point."""
+    M, K = x.shape
+    N = lin.w.shape[0]
+    _lib.call("wf_w8a8_linear", x.data_ptr(), M, K, x.stride(0), lin.w.data_ptr(), lin.s.data_ptr(),
+              _lib.ptr(lin.b), N, out.data_ptr(), out.stride(0), _lib.GEMM_GELU_TANH if gelu else 0,
+              ws_q.data_ptr(), ws_s.data_ptr(), _lib.stream_handle(x.device))
+    return out
+
+
+class QuantizedWanBlock:
+    """One Wan block with quantized weights resident on the GPU."""
+
+    def __init__(self, params: BlockParams, heads: int, device="cuda") -> None:
+        self.device = torch.device(device)
+        self.dim = params.dim
+        self.heads = heads
+        self.head_dim = self.dim // heads
+        self.ffn_dim = params.fc_in_w.shape[0]
+        dev = self.device
+        self.modulation = params.modulation.to(dev)
+        self.qkv = QLinear.from_bf16(torch.cat([params.q_w, params.k_w, params.v_w], 0),
+                                     torch.cat([params.q_b, params.k_b, params.v_b], 0), dev)
+        self.o = QLinear.from_bf16(params.o_w, params.o_b, dev)
+        self.cq = QLinear.from_bf16(params.cq_w, params.cq_b, dev)
+        self.ck = QLinear.from_bf16(params.ck_w, params.ck_b, dev)
+        self.cv = QLinear.from_bf16(params.cv_w, params.cv_b, dev)
+        self.co = QLinear.from_bf16(params.co_w, params.co_b, dev)
+        self.fc_in = QLinear.from_bf16(params.fc_in_w, params.fc_in_b, dev)
+        self.fc_out = QLinear.from_bf16(params.fc_out_w, params.fc_out_b, dev)
+        self.norm_q = params.norm_q.to(dev)
+        self.norm_k = params.norm_k.to(dev)
+        self.norm3_w = params.norm3_w.to(dev)
+        self.norm3_b = params.norm3_b.to(dev)
+        self.cnorm_q = params.cnorm_q.to(dev)
+        self.cnorm_k = params.cnorm_k.to(dev)
+        self._ws: dict = {}
+
+    # -- workspace (allocated once per token count; the kernels never allocate)
+    def _workspace(self, T: int) -> dict:
+        ws = self._ws.get(T)
+        if ws is None:
+            dev, dim = self.device, self.dim
+            bf = dict(dtype=torch.bfloat16, device=dev)
+            qbuf = torch.empty((T * max(dim, self.ffn_dim),), dtype=torch.int8, device=dev)
+            ws = dict(
+                aq=qbuf[:T * dim].view(T, dim), fq=qbuf[:T * self.ffn_dim].view(T, self.ffn_dim),
+                as_=torch.empty((T,), dtype=torch.float32, device=dev),
+                qkv=torch.empty((T, 3 * dim), **bf), attn=torch.empty((T, dim), **bf), y=torch.empty((T, dim), **bf),
+                cq=torch.empty((T, dim), **bf), ffn=torch.empty((T, self.ffn_dim), **bf),
+            )
+            self._ws[T] = ws
+        return ws
+
+    def text_kv(self, context: torch.Tensor):
+        """Cross-attention K/V of the text context [L, dim] (computed once per request)."""
+        L = context.shape[0]
+        dev = self.device
+        ws_q = torch.empty((L, self.dim), dtype=torch.int8, device=dev)
+        ws_s = torch.empty((L,), dtype=torch.float32, device=dev)
+        k = torch.empty((L, self.dim), dtype=torch.bfloat16, device=dev)
+        v = torch.empty((L, self.dim), dtype=torch.bfloat16, device=dev)
+        _linear_i8(context, self.ck, ws_q, ws_s, k)
+        kn = torch.empty_like(k)
+        _rmsnorm_rope(k, self.head_dim, self.cnorm_k, None, None, kn)
+        _linear_i8(context, self.cv, ws_q, ws_s, v)
+        return kn.view(L, self.heads, self.head_dim), v.view(L, self.heads, self.head_dim)
+
+    def forward(self, x: torch.Tensor, e: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pool: Fp8PagePool,
+                context_table: PageTable, own_table: PageTable, n_context: int, text_kv) -> torch.Tensor:
+        """Advance x [T, dim] bf16 in place through the block.
+
+        e: [F, 6, dim] bf16 time modulation of the chunk's F frames.
+        cos/sin: RoPE tables [T, head_dim/2] of this chunk.
+        pool/context_table/n_context: this layer's FP8 page context (prior
+        chunks' pages followed by ``own_table``'s pages), of n_context keys
+        including this chunk's T tokens, which are packed into own_table here.
+        """
+        T, dim = x.shape
+        F = e.shape[0]
+        if T % F:
+            raise ValueError(f"{T} tokens do not split into {F} frames")
+        ft = T // F
+        H, hd = self.heads, self.head_dim
+        ws = self._workspace(T)
+        # e = (modulation + e).chunk(6)  (causal_model.py:376), bf16
+        es = (self.modulation[0].unsqueeze(0) + e).contiguous()
+        e0, e1, e2, e3, e4, e5 = (es[:, i].contiguous() for i in range(6))
+        aq, as_ = ws["aq"], ws["as_"]
+
+        # self-attention: LN1 + modulation + int8 quant -> fused QKV
+        _ln_quant(x, dim, ft, aq, as_, shift=e0, scale=e1)
+        gemm_i8(aq, self.qkv.w, as_, self.qkv.s, self.qkv.b, out=ws["qkv"])
+        qkv = ws["qkv"]
+        q, k, v = qkv[:, :dim], qkv[:, dim:2 * dim], qkv[:, 2 * dim:]
+        # in place: each row is read whole before its reduction, written after
+        _rmsnorm_rope(q, hd, self.norm_q, cos, sin, q)
+        _rmsnorm_rope(k, hd, self.norm_k, cos, sin, k)
+        pool.pack(k.view(T, H, hd), v.view(T, H, hd), own_table)
+        ctx = PagedKV(pool, context_table, n_context)
+        attn_paged_fp8(q.view(T, H, hd), ctx, out=ws["attn"].view(T, H, hd))
+        _linear_i8(ws["attn"], self.o, aq, as_, ws["y"])
+        _gate_residual(x, ws["y"], e2, ft)
+
+        # cross-attention: norm3 (affine) + quant -> q, RMSNorm, attention over text, o
+        _ln_quant(x, dim, ft, aq, as_, w=self.norm3_w, b=self.norm3_b)
+        gemm_i8(aq, self.cq.w, as_, self.cq.s, self.cq.b, out=ws["y"])
+        _rmsnorm_rope(ws["y"], hd, self.cnorm_q, None, None, ws["cq"])
+        tk, tv = text_kv
+        attn_dense_bf16(ws["cq"].view(T, H, hd), tk, tv, out=ws["attn"].view(T, H, hd))
+        _linear_i8(ws["attn"], self.co, aq, as_, ws["y"])
+        _gate_residual(x, ws["y"], None, ft)
+
+        # FFN: LN2 + modulation + quant -> fc_in (+GELU) -> fc_out
+        _ln_quant(x, dim, ft, aq, as_, shift=e3, scale=e4)
+        gemm_i8(aq, self.fc_in.w, as_, self.fc_in.s, self.fc_in.b, gelu=True, out=ws["ffn"])
+        _linear_i8(ws["ffn"], self.fc_out, ws["fq"], as_, ws["y"])
+        _gate_residual(x, ws["y"], e5, ft)
+        return x

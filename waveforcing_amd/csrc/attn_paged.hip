@@ -61,6 +61,9 @@ struct AttnArgs {
   const float* k_scales;
   const float* v_scales;
   const int32_t* table;
+  const uint16_t* k_dense;  // dense bf16 K [n_kv, ldkv] (dense-context variant)
+  const uint16_t* v_dense;
+  int64_t ldkv;
   uint16_t* out;  // bf16 [Lq, ldo] with head h at offset h * D
   int64_t ldo;
   int Lq, H, n_kv, n_table, page_tokens, pool_pages;
@@ -104,7 +107,7 @@ __device__ inline void static_for(F&& f) {
 
 // WAVES waves of 32 queries each share one decoded K/V tile; PGR register
 // buffers let the loads of tile it + PGR fly while tile it computes.
-template <int WAVES, int PGR>
+template <int WAVES, int PGR, bool DENSE>
 __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(AttnArgs p) {
   constexpr int THREADS = WAVES * 64;
   constexpr int BQ = WAVES * 32;
@@ -175,9 +178,43 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
   u32x4 rk_code[PGR][KCH];
   uint32_t rv_code[PGR][VT][4];
   float rscale[PGR];
+  // second halves of the dense bf16 variant's staging (unused for FP8 pages)
+  u32x4 rk_hi[DENSE ? PGR : 1][DENSE ? KCH : 1];
+  uint32_t rv_hi[DENSE ? PGR : 1][DENSE ? VT : 1][4];
 
   auto load_tile = [&](auto buf, int t0) {
     constexpr int u = decltype(buf)::value;
+    if constexpr (DENSE) {
+      // K: 16 bf16 = two 16-byte halves per chunk; V: 4 keys x 4 d (8 bytes per key)
+      const int kv_bytes = p.n_kv * static_cast<int>(p.ldkv) * 2;
+      const __amdgpu_buffer_rsrc_t rkd =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.k_dense), 0, kv_bytes, kBufferRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rvd =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.v_dense), 0, kv_bytes, kBufferRsrcWord3);
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        const int c = tid + THREADS * i;
+        const int key = t0 + (c >> 3);
+        const int off = key < p.n_kv ? (key * static_cast<int>(p.ldkv) + h * D + (c & 7) * 16) * 2 : kOutOfRange;
+        rk_code[u][i] = __builtin_amdgcn_raw_buffer_load_b128(rkd, off, 0, 0);
+        rk_hi[u][i] = __builtin_amdgcn_raw_buffer_load_b128(rkd, off == kOutOfRange ? off : off + 16, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < VT; ++i) {
+        const int task = tid + THREADS * i;
+        const int kg = task >> 5, d0 = (task & 31) * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = t0 + 4 * kg + j;
+          const int off = key < p.n_kv ? (key * static_cast<int>(p.ldkv) + h * D + d0) * 2 : kOutOfRange;
+          const auto w2 = __builtin_amdgcn_raw_buffer_load_b64(rvd, off, 0, 0);
+          rv_code[u][i][j] = w2[0];
+          rv_hi[u][i][j] = w2[1];
+        }
+      }
+      rscale[u] = (t0 + (tid & (BKV - 1)) < p.n_kv) ? 1.0f : 0.0f;
+      return;
+    }
     map_tile(t0);
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
@@ -208,6 +245,32 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
     uint8_t* sk = lds + lbuf * STAGE;
     uint8_t* sv = sk + K_TILE;
     float* ss = reinterpret_cast<float*>(sv + V_TILE);
+    if constexpr (DENSE) {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        const int c = tid + THREADS * i;
+        uint4* dst = reinterpret_cast<uint4*>(sk + (c >> 3) * KP + (c & 7) * 32);
+        dst[0] = make_uint4(rk_code[u][i][0], rk_code[u][i][1], rk_code[u][i][2], rk_code[u][i][3]);
+        dst[1] = make_uint4(rk_hi[u][i][0], rk_hi[u][i][1], rk_hi[u][i][2], rk_hi[u][i][3]);
+      }
+#pragma unroll
+      for (int i = 0; i < VT; ++i) {
+        const int task = tid + THREADS * i;
+        const int kg = task >> 5, d0 = (task & 31) * 4;
+        const int pos = ((kg & ~3) * 4 + ((kg & 1) << 3) + ((kg & 2) << 1)) ^ vswz(d0);
+        // key j holds d0, d0+1 in rv_code[j] and d0+2, d0+3 in rv_hi[j]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t* src = (j < 2) ? rv_code[u][i] : rv_hi[u][i];
+          const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;  // high or low bf16 of each key word
+          const uint32_t lo = __builtin_amdgcn_perm(src[1], src[0], sel);
+          const uint32_t hi = __builtin_amdgcn_perm(src[3], src[2], sel);
+          *reinterpret_cast<uint2*>(sv + (d0 + j) * VP + pos * 2) = make_uint2(lo, hi);
+        }
+      }
+      if (tid < 2 * BKV) ss[tid] = tid < BKV ? rscale[u] * p.qk_scale : rscale[u];
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = tid + THREADS * i;
@@ -382,12 +445,12 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
 
 }  // namespace
 
-template <int WAVES, int PGR>
+template <int WAVES, int PGR, bool DENSE = false>
 int launch_attn(const AttnArgs& p, int64_t lq, int n_heads, hipStream_t stream) {
   const int64_t items = (lq + WAVES * 32 - 1) / (WAVES * 32) * n_heads;
   const dim3 grid(static_cast<uint32_t>((items + 7) / 8 * 8));
-  hipLaunchKernelGGL((attn_paged_fp8_kernel<WAVES, PGR>), grid, dim3(WAVES * 64), 0, stream, p);
-  return check_launch("wf_attn_paged_fp8");
+  hipLaunchKernelGGL((attn_paged_fp8_kernel<WAVES, PGR, DENSE>), grid, dim3(WAVES * 64), 0, stream, p);
+  return check_launch(DENSE ? "wf_attn_dense_bf16" : "wf_attn_paged_fp8");
 }
 
 }  // namespace wf
@@ -424,6 +487,9 @@ extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int
   p.k_scales = k_scales;
   p.v_scales = v_scales;
   p.table = page_table;
+  p.k_dense = nullptr;
+  p.v_dense = nullptr;
+  p.ldkv = 0;
   p.out = static_cast<uint16_t*>(out);
   p.ldo = ldo;
   p.Lq = static_cast<int>(lq);
@@ -438,4 +504,36 @@ extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int
   // prefetch: the best of {4, 8} waves x {1, 2} tiles of prefetch measured on
   // the 1.3B / 14B context shapes.
   return wf::launch_attn<8, 1>(p, lq, n_heads, wf::as_stream(stream));
+}
+
+extern "C" int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads, int32_t head_dim, int64_t ldq,
+                                  const void* k, const void* v, int64_t n_kv, int64_t ldkv, float softmax_scale,
+                                  void* out, int64_t ldo, void* stream) {
+  static const char* fn = "wf_attn_dense_bf16";
+  WF_REQUIRE(lq >= 0 && n_heads > 0 && n_kv >= 0, WF_E_INVALID, "%s: negative or zero size", fn);
+  WF_REQUIRE(head_dim == wf::D, WF_E_SHAPE, "%s: head_dim=%d unsupported (must be 128)", fn, head_dim);
+  const int64_t hd = static_cast<int64_t>(n_heads) * head_dim;
+  WF_REQUIRE(ldq >= hd && ldo >= hd && ldkv >= hd, WF_E_INVALID, "%s: row strides smaller than n_heads*head_dim", fn);
+  if (lq == 0) return WF_OK;
+  WF_REQUIRE(q && out && (n_kv == 0 || (k && v)), WF_E_INVALID, "%s: null pointer", fn);
+  WF_REQUIRE(n_kv * ldkv * 2 < (1ll << 31) - 16 && lq < (1ll << 31), WF_E_SHAPE, "%s: K/V of 2 GiB or more", fn);
+  WF_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15u) == 0 && ldq % 8 == 0 && (reinterpret_cast<uintptr_t>(k) & 15u) == 0 &&
+                 (reinterpret_cast<uintptr_t>(v) & 15u) == 0 && ldkv % 8 == 0 &&
+                 (reinterpret_cast<uintptr_t>(out) & 7u) == 0 && ldo % 4 == 0,
+             WF_E_ALIGN, "%s: q, k, v must be 16-byte aligned (strides %% 8 == 0), out 8-byte aligned", fn);
+  wf::AttnArgs p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.ldq = ldq;
+  p.k_dense = static_cast<const uint16_t*>(k);
+  p.v_dense = static_cast<const uint16_t*>(v);
+  p.ldkv = ldkv;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  p.Lq = static_cast<int>(lq);
+  p.H = n_heads;
+  p.n_kv = static_cast<int>(n_kv);
+  p.page_tokens = 1;
+  p.page_div = wf::FastDiv(1);
+  p.qk_scale = softmax_scale * wf::kLog2e;
+  return wf::launch_attn<8, 1, true>(p, lq, n_heads, wf::as_stream(stream));
 }

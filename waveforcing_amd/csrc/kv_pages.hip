@@ -119,7 +119,7 @@ __device__ inline void st16(uint4* p, const uint4& v) {
 // ROWS rows per lane group; a workgroup owns 32 * ROWS consecutive rows.
 template <int ROWS, bool NT_LOAD, bool NT_STORE>
 __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ k, const uint4* __restrict__ v,
-                                                      uint32_t n_rows, PageGeom geom, PoolView kpool,
+                                                      int64_t ld_kv, uint32_t n_rows, PageGeom geom, PoolView kpool,
                                                       PoolView vpool) {
   const uint4* __restrict__ src = blockIdx.y == 0 ? k : v;
   const PoolView pool = blockIdx.y == 0 ? kpool : vpool;
@@ -131,7 +131,9 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ 
   for (int u = 0; u < ROWS; ++u) {
     const uint32_t r = row0 + 32u * u;
     if (r < n_rows) {
-      const uint4* p = src + static_cast<int64_t>(r) * (kHeadDim / 8) + lane8 * 2;
+      uint32_t t, h;
+      geom.heads.divmod(r, t, h);
+      const uint4* p = src + (static_cast<int64_t>(t) * ld_kv + h * kHeadDim) / 8 + lane8 * 2;
       a[u] = ld16<NT_LOAD>(p);
       b[u] = ld16<NT_LOAD>(p + 1);
     } else {
@@ -243,13 +245,15 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 extern "C" {
 
 int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
-                   const int32_t* page_table, int64_t n_table, int32_t page_tokens, uint8_t* k_codes,
+                   int64_t ld_kv, const int32_t* page_table, int64_t n_table, int32_t page_tokens, uint8_t* k_codes,
                    uint8_t* v_codes, float* k_scales, float* v_scales, int64_t pool_pages, void* stream) {
   static const char* fn = "wf_fp8_kv_pack";
   if (int st = wf::check_pool_args(fn, n_tokens, n_heads, head_dim, page_table, n_table, page_tokens, pool_pages))
     return st;
   if (n_tokens == 0) return WF_OK;
   WF_REQUIRE(k && k_codes && k_scales, WF_E_INVALID, "%s: null K pointer", fn);
+  WF_REQUIRE(ld_kv >= static_cast<int64_t>(n_heads) * head_dim && ld_kv % 8 == 0, WF_E_INVALID,
+             "%s: ld_kv=%lld must be >= n_heads*head_dim and a multiple of 8", fn, (long long)ld_kv);
   const bool has_v = v != nullptr;
   WF_REQUIRE(!has_v || (v_codes && v_scales), WF_E_INVALID, "%s: V given without V pool", fn);
   WF_REQUIRE(wf::aligned16(k) && wf::aligned16(k_codes) && (!has_v || (wf::aligned16(v) && wf::aligned16(v_codes))),
@@ -259,7 +263,7 @@ int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_hea
   constexpr int kRows = wf::kPackRows;
   const dim3 grid((n_rows + 32 * kRows - 1) / (32 * kRows), has_v ? 2 : 1);
   hipLaunchKernelGGL((wf::kv_pack_kernel<kRows, wf::kPackNtLoad, wf::kPackNtStore>), grid, dim3(256), 0, wf::as_stream(stream),
-                     reinterpret_cast<const uint4*>(k), reinterpret_cast<const uint4*>(v), n_rows, geom,
+                     reinterpret_cast<const uint4*>(k), reinterpret_cast<const uint4*>(v), ld_kv, n_rows, geom,
                      wf::PoolView{k_codes, k_scales}, wf::PoolView{v_codes, v_scales});
   return wf::check_launch(fn);
 }

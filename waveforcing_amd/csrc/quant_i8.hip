@@ -14,12 +14,11 @@
 // those elements are recomputed with a full IEEE division, so the result is
 // round_half_even(RN(x / s)) exactly.
 //
-// One workgroup (256 threads) per row for long rows: each thread owns 16
-// consecutive bf16 (two 16-byte loads) and writes 16 int8 codes (one
-// 16-byte store) per pass.  The row is read from HBM once and kept in
-// registers between the amax reduction and the quantization pass when
-// K <= 4096 (the 1.3B/14B widths up to 4096); longer rows take a second
-// read (served by L2).
+// One wave per row, 4 rows per 256-thread workgroup: each lane owns chunks
+// of 8 consecutive bf16 (one 16-byte load, one 8-byte store of codes); rows
+// up to 4096 wide stay in registers between the absmax reduction (a wave64
+// butterfly, no LDS) and the quantization pass, longer rows are read twice
+// (the second read is served by L2).
 #include "launchers.hpp"
 #include "wf_common.hpp"
 
@@ -27,18 +26,12 @@ namespace wf {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kElemsPerThread = 16;
-constexpr int kRegPasses = 1;  // 4096 elements per row held in registers
+constexpr int kRowsPerBlock = kThreads / 64;
+constexpr int kRegChunks = 8;  // 8 chunks x 8 elements x 64 lanes = 4096 per row in registers
 
-__device__ inline float row_reduce_max(float v, float* red) {
-  // wave64: butterfly via DPP-free shuffles (cheap at this volume)
+__device__ inline float wave_max(float v) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  float m = red[0];
-  for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w]);
-  return m;
+  return v;
 }
 
 __device__ inline int8_t quant_one(float x, float s, float r) {
@@ -54,37 +47,19 @@ __device__ inline int8_t quant_one(float x, float s, float r) {
   return static_cast<int8_t>(static_cast<int>(qi));
 }
 
-__device__ inline void load16(const uint16_t* row, int64_t k0, int64_t K, uint4& a, uint4& b) {
-  if (k0 + 16 <= K) {
-    const uint4* p = reinterpret_cast<const uint4*>(row + k0);
-    a = p[0];
-    b = p[1];
-  } else {
-    uint32_t w[8];
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t lo = (k0 + 2 * i < K) ? row[k0 + 2 * i] : 0u;
-      const uint32_t hi = (k0 + 2 * i + 1 < K) ? row[k0 + 2 * i + 1] : 0u;
-      w[i] = lo | (hi << 16);
-    }
-    a = make_uint4(w[0], w[1], w[2], w[3]);
-    b = make_uint4(w[4], w[5], w[6], w[7]);
-  }
-}
-
-__device__ inline float amax16(const uint4& a, const uint4& b) {
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+__device__ inline float amax8(const uint4& a) {
+  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
   float m = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) m = fmaxf(m, fmaxf(fabsf(bf16_lo_to_f32(w[i])), fabsf(bf16_hi_to_f32(w[i]))));
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bf16_lo_to_f32(w[i])), fabsf(bf16_hi_to_f32(w[i]))));
   return m;
 }
 
-__device__ inline void quant16_store(const uint4& a, const uint4& b, float s, float r, int8_t* out, int64_t k0,
-                                     int64_t K) {
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  uint32_t packed[4];
+__device__ inline uint2 quant8(const uint4& a, float s, float r) {
+  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+  uint32_t packed[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2; ++i) {
     const int8_t q0 = quant_one(bf16_lo_to_f32(w[2 * i]), s, r);
     const int8_t q1 = quant_one(bf16_hi_to_f32(w[2 * i]), s, r);
     const int8_t q2 = quant_one(bf16_lo_to_f32(w[2 * i + 1]), s, r);
@@ -94,63 +69,49 @@ __device__ inline void quant16_store(const uint4& a, const uint4& b, float s, fl
                 (static_cast<uint32_t>(static_cast<uint8_t>(q2)) << 16) |
                 (static_cast<uint32_t>(static_cast<uint8_t>(q3)) << 24);
   }
-  if (k0 + 16 <= K) {
-    *reinterpret_cast<uint4*>(out + k0) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-  } else {
-    for (int i = 0; i < 16 && k0 + i < K; ++i) out[k0 + i] = static_cast<int8_t>(packed[i / 4] >> (8 * (i % 4)));
-  }
+  return make_uint2(packed[0], packed[1]);
 }
 
+// K % 8 == 0 (checked at the entry point): every 8-element chunk is whole.
 __global__ __launch_bounds__(kThreads) void quant_rows_i8_kernel(const uint16_t* __restrict__ x, int64_t M,
                                                                  int64_t K, int64_t ldx, int8_t* __restrict__ q,
                                                                  int64_t ldq, float* __restrict__ scales) {
-  __shared__ float red[kThreads / 64];
-  const int64_t m = blockIdx.x;
-  if (m >= M) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (m >= M) return;  // whole wave exits together
   const uint16_t* row = x + m * ldx;
   int8_t* qrow = q + m * ldq;
-  const int64_t span = static_cast<int64_t>(kThreads) * kElemsPerThread;
-  const int64_t k_first = static_cast<int64_t>(threadIdx.x) * kElemsPerThread;
+  const int64_t n_chunks = K / 8;
 
-  uint4 ra[kRegPasses], rb[kRegPasses];
+  uint4 reg[kRegChunks];
   float amax = 0.f;
 #pragma unroll
-  for (int p = 0; p < kRegPasses; ++p) {
-    const int64_t k0 = k_first + p * span;
-    if (k0 < K) {
-      load16(row, k0, K, ra[p], rb[p]);
-      amax = fmaxf(amax, amax16(ra[p], rb[p]));
-    } else {
-      ra[p] = make_uint4(0, 0, 0, 0);
-      rb[p] = ra[p];
-    }
+  for (int c = 0; c < kRegChunks; ++c) {
+    const int64_t ch = lane + 64 * c;
+    reg[c] = ch < n_chunks ? *reinterpret_cast<const uint4*>(row + ch * 8) : make_uint4(0, 0, 0, 0);
+    amax = fmaxf(amax, amax8(reg[c]));
   }
-  for (int64_t k0 = k_first + kRegPasses * span; k0 < K; k0 += span) {
-    uint4 a, b;
-    load16(row, k0, K, a, b);
-    amax = fmaxf(amax, amax16(a, b));
-  }
-  amax = row_reduce_max(amax, red);
+  for (int64_t ch = lane + 64 * kRegChunks; ch < n_chunks; ch += 64)
+    amax = fmaxf(amax, amax8(*reinterpret_cast<const uint4*>(row + ch * 8)));
+  amax = wave_max(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-8f);
   const float r = __frcp_rn(s);
-  if (threadIdx.x == 0) scales[m] = s;
+  if (lane == 0) scales[m] = s;
 #pragma unroll
-  for (int p = 0; p < kRegPasses; ++p) {
-    const int64_t k0 = k_first + p * span;
-    if (k0 < K) quant16_store(ra[p], rb[p], s, r, qrow, k0, K);
+  for (int c = 0; c < kRegChunks; ++c) {
+    const int64_t ch = lane + 64 * c;
+    if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(reg[c], s, r);
   }
-  for (int64_t k0 = k_first + kRegPasses * span; k0 < K; k0 += span) {
-    uint4 a, b;
-    load16(row, k0, K, a, b);
-    quant16_store(a, b, s, r, qrow, k0, K);
-  }
+  for (int64_t ch = lane + 64 * kRegChunks; ch < n_chunks; ch += 64)
+    *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(*reinterpret_cast<const uint4*>(row + ch * 8), s, r);
 }
 
 }  // namespace
 
 int launch_quant_rows_i8(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* scales,
                          hipStream_t stream) {
-  hipLaunchKernelGGL(quant_rows_i8_kernel, dim3(static_cast<uint32_t>(M)), dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL(quant_rows_i8_kernel, dim3(static_cast<uint32_t>((M + kRowsPerBlock - 1) / kRowsPerBlock)),
+                     dim3(kThreads), 0, stream,
                      static_cast<const uint16_t*>(x), M, K, ldx, q, ldq, scales);
   return check_launch("wf_quant_rows_i8");
 }

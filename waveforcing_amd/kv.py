@@ -47,7 +47,11 @@ class PageTable:
 
 
 def _as_thd(x: torch.Tensor, name: str) -> torch.Tensor:
-    """Accept [T, H, D] or the reference's [1, T, H, D] views (paged.py:207-208)."""
+    """Accept [T, H, D] or the reference's [1, T, H, D] views (paged.py:207-208).
+
+    Heads and head_dim must be dense; the token stride may be larger (e.g. a
+    column slice of a fused QKV output) as long as it is a multiple of 8.
+    """
     if x.dim() == 4:
         if x.shape[0] != 1:
             raise ValueError(f"{name}: batch dimension must be 1, got {tuple(x.shape)}")
@@ -56,7 +60,10 @@ def _as_thd(x: torch.Tensor, name: str) -> torch.Tensor:
         raise ValueError(f"{name}: expected [T, H, D], got {tuple(x.shape)}")
     if x.dtype != torch.bfloat16:
         raise ValueError(f"{name}: expected bfloat16, got {x.dtype}")
-    return x.contiguous()
+    T, H, D = x.shape
+    if x.stride(2) != 1 or x.stride(1) != D or x.stride(0) % 8 or x.data_ptr() % 16 or (T > 1 and x.stride(0) < H * D):
+        x = x.contiguous()
+    return x
 
 
 class Fp8PagePool:
@@ -106,9 +113,14 @@ class Fp8PagePool:
             raise ValueError(f"k has H={H}, D={D}; pool has H={self.n_heads}, D={self.head_dim}")
         if len(table) * self.page_tokens < T:
             raise RuntimeError(f"page table of {len(table)} pages cannot hold {T} tokens")
+        # one token stride serves K and V; if they differ, fall back to dense copies
+        ld = k.stride(0) if T > 1 else H * D
+        if v is not None and (v.stride(0) if T > 1 else H * D) != ld:
+            k, v = k.contiguous(), v.contiguous()
+            ld = H * D
         _lib.call(
             "wf_fp8_kv_pack",
-            _lib.ptr(k), _lib.ptr(v), T, H, D,
+            _lib.ptr(k), _lib.ptr(v), T, H, D, ld,
             table.dev.data_ptr(), len(table), self.page_tokens,
             self.k_codes.data_ptr(), self.v_codes.data_ptr() if v is not None else None,
             self.k_scales.data_ptr(), self.v_scales.data_ptr() if v is not None else None,
