@@ -41,6 +41,17 @@ BF16_PEAK_TFLOPS = 2500.0
 LAYERS, TOKENS, HEADS, HEAD_DIM, PAGE = 30, 4680, 12, 128, 1560
 
 
+def profiled_traffic(name: str):
+    """HBM bytes per launch recorded by the PMC runs summarized in profiles/<name>.md, or None."""
+    path = os.path.join(ROOT, "profiles", name + ".md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1].split()[0]))
+    return None
+
+
 def kv_bytes_per_layer() -> int:
     """Algorithmic bytes of packing (or unpacking) one layer's K and V."""
     elems = TOKENS * HEADS * HEAD_DIM
@@ -63,7 +74,7 @@ def _timed(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(stop) / steps
 
 
-def bench_kv(steps: int, warmup: int, dev: str):
+def bench_kv(steps: int, warmup: int, dev: str, which=("pack", "unpack", "pack_layers", "unpack_layers")):
     """Pack / gather-dequant of 30 layers: one launch over all layers (the
     headline) and one launch per layer (the exchange's per-layer publish)."""
     ppl = TOKENS // PAGE
@@ -99,9 +110,8 @@ def bench_kv(steps: int, warmup: int, dev: str):
             pool.unpack(tables[layer], TOKENS, out_k=ko_all[sl], out_v=vo_all[sl])
 
     step_bytes = LAYERS * kv_bytes_per_layer()
-    ms = {name: _timed(fn, steps, warmup) for name, fn in
-          (("pack", pack_all), ("unpack", unpack_all), ("pack_layers", pack_layers),
-           ("unpack_layers", unpack_layers))}
+    fns = {"pack": pack_all, "unpack": unpack_all, "pack_layers": pack_layers, "unpack_layers": unpack_layers}
+    ms = {name: _timed(fns[name], steps, warmup) for name in which}
     out = {"bytes_per_step": step_bytes}
     for name, t in ms.items():
         out[f"ms_{name}"] = t
@@ -187,6 +197,14 @@ def bench_block(scale: str, steps: int, warmup: int, dev: str):
     return {"ms": ms, "tokens": T, "context_keys": (prior + 1) * T}
 
 
+def bench_copy(steps: int, warmup: int, dev: str):
+    """A plain device copy of 1 GiB (read 1 GiB + write 1 GiB): calibrates the HBM byte counters."""
+    src = torch.empty((1 << 30,), dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = _timed(lambda: dst.copy_(src), steps, warmup)
+    return {"ms": ms, "bytes_read": 1 << 30, "bytes_written": 1 << 30, "gbs": 2 * (1 << 30) / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline_kv() -> dict:
     """Oracle torch-CPU pack (quantize + page scatter) of a bounded sample of layers."""
     from oracle import kv as okv
@@ -230,6 +248,9 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "attention", "block_1p3b", "block_14b",
+                                       "copy"],
+                    help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path runs on a single GPU); --gpus {args.gpus} is not supported",
@@ -239,6 +260,13 @@ def main() -> None:
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = "cuda:0"
+    if args.only:
+        fn = {"kv": bench_kv, "kv_pack": lambda s, w, d: bench_kv(s, w, d, ("pack",)),
+              "kv_unpack": lambda s, w, d: bench_kv(s, w, d, ("unpack",)), "gemm": bench_gemm, "attention": bench_attention, "copy": bench_copy,
+              "block_1p3b": lambda s, w, d: bench_block("1.3b", s, w, d),
+              "block_14b": lambda s, w, d: bench_block("14b", s, w, d)}[args.only]
+        print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
+        return
     kv = bench_kv(args.steps, args.warmup, dev)
     gm = bench_gemm(args.steps, args.warmup, dev)
     at = bench_attention(args.steps, args.warmup, dev)
@@ -271,7 +299,7 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic("fp8_kv_pack_30_layers"),
         },
         "cpu_baseline": cpu,
         "extra": {
