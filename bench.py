@@ -245,8 +245,8 @@ def cpu_baseline_kv() -> dict:
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "attention", "block_1p3b", "block_14b",
                                        "copy"],
@@ -268,10 +268,10 @@ def main() -> None:
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
     kv = bench_kv(args.steps, args.warmup, dev)
-    gm = bench_gemm(args.steps, args.warmup, dev)
-    at = bench_attention(args.steps, args.warmup, dev)
-    b13 = bench_block("1.3b", args.steps, args.warmup, dev)
-    b14 = bench_block("14b", max(3, args.steps // 4), 1, dev)
+    gm = bench_gemm(max(5, args.steps // 5), 2, dev)
+    at = bench_attention(max(5, args.steps // 5), 2, dev)
+    b13 = bench_block("1.3b", max(5, args.steps // 5), 2, dev)
+    b14 = bench_block("14b", max(3, args.steps // 10), 1, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     # one launch per step: the launch duration is the step time
     achieved = kv["bytes_per_step"] / (kv["ms_pack"] * 1e-3) / 1e9

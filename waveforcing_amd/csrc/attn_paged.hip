@@ -15,7 +15,7 @@
 // head; each wave owns 32 queries.  Keys advance in tiles of 64.  Per tile the workgroup
 // loads the K and V codes of the tile (through buffer descriptors over the
 // pools: keys past n_kv or on invalid pages read as zero) and the per-key
-// scales, decodes the codes once to bf16 (exact) into LDS, K as [key][d] and
+// scales, dequantizes the codes once to bf16 into LDS, K as [key][d] and
 // V transposed as [d][key'] with the key order permuted within each group of
 // 16 (key bits 2 and 3 swapped) so that the PV operand fragment is one
 // 16-byte read that matches the register layout of P.
@@ -25,9 +25,9 @@
 // Q^T kept in registers for the whole kernel): each lane then holds one
 // query column and 16 keys per 32-key block, so the online-softmax row max
 // is an in-lane max plus one exchange with lane ^ 32, and the lane's P values
-// are directly the second operand of O^T = V^T P^T.  s_k (times
-// scale * log2 e) scales S^T rows, s_v scales P^T rows before the bf16
-// rounding of P; the row sum uses the unscaled P.
+// are directly the second operand of O^T = V^T P^T.  K and V enter LDS as
+// bf16(code * s), the pages' gather-dequant values; the softmax works in
+// base 2 with the scale folded into one FMA per score.
 #include <utility>
 
 #include "fastdiv.hpp"
@@ -47,8 +47,7 @@ constexpr int KP = D * 2 + 16;   // K tile row pitch (bytes, bf16 + pad) = 272
 constexpr int VP = BKV * 2 + 16; // V^T tile row pitch (bytes) = 144
 constexpr int K_TILE = BKV * KP;
 constexpr int V_TILE = D * VP;
-constexpr int S_TILE = 2 * BKV * 4;  // c*s_k then s_v (fp32)
-constexpr int STAGE = K_TILE + V_TILE + S_TILE;
+constexpr int STAGE = K_TILE + V_TILE;
 constexpr int kBufferRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
 constexpr int kOutOfRange = 0x7ffffff0;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -87,6 +86,14 @@ __device__ inline uint32_t cvt_bf16x2(float lo, float hi) {
   typedef __bf16 b2 __attribute__((ext_vector_type(2)));
   const f2 v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
+}
+
+// Dequantize 4 e4m3 codes (bytes of w) with per-code scales into 2 dwords of
+// packed bf16: bf16_rne(float(code) * s), the pages' gather-dequant value.
+__device__ inline uint2 dequant4_bf16(uint32_t w, float s0, float s1, float s2, float s3) {
+  float a, b, c, d;
+  e4m3_unpack4_hw(w, a, b, c, d);
+  return make_uint2(cvt_bf16x2(a * s0, b * s1), cvt_bf16x2(c * s2, d * s3));
 }
 
 // Decode 4 e4m3 codes (bytes of w) into 2 dwords of packed bf16.
@@ -143,41 +150,45 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
   const __amdgpu_buffer_rsrc_t rsv =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.v_scales), 0, scale_bytes, kBufferRsrcWord3);
 
-  // A 64-key tile spans at most two pages (page_tokens >= 64, checked on
-  // the host): resolve them once per tile, then each key is a compare.
-  int tile_page0 = -1, tile_page1 = -1, tile_rip0 = 0, tile_t0 = 0;
+  // A 64-key tile spans at most two pages (page_tokens >= 64, checked on the
+  // host).  map_tile resolves them once per tile into base offsets (uniform
+  // across the workgroup); a key k of the tile is then one compare and one
+  // multiply-add.  Offsets of keys past n_kv or on invalid pages are pushed
+  // out of the buffer range, so they read as zero.
+  const int HD = p.H * D;
+  int t_split = 0, t_valid = 0, t_cb0 = 0, t_cb1 = 0, t_sb0 = 0, t_sb1 = 0;
+  bool t_ok0 = false, t_ok1 = false;
   auto map_tile = [&](int t0) {
     uint32_t lp, rip;
     p.page_div.divmod(static_cast<uint32_t>(t0), lp, rip);
-    tile_t0 = t0;
-    tile_rip0 = static_cast<int>(rip);
     const int pg0 = static_cast<int>(lp) < p.n_table ? p.table[lp] : -1;
     const int pg1 = static_cast<int>(lp) + 1 < p.n_table ? p.table[lp + 1] : -1;
-    tile_page0 = (pg0 >= 0 && pg0 < p.pool_pages) ? pg0 : -1;
-    tile_page1 = (pg1 >= 0 && pg1 < p.pool_pages) ? pg1 : -1;
+    t_ok0 = pg0 >= 0 && pg0 < p.pool_pages;
+    t_ok1 = pg1 >= 0 && pg1 < p.pool_pages;
+    t_split = p.page_tokens - static_cast<int>(rip);
+    t_valid = p.n_kv - t0;
+    t_cb0 = t_ok0 ? ((pg0 * p.page_tokens + static_cast<int>(rip)) * p.H + h) * D : 0;
+    t_cb1 = t_ok1 ? (pg1 * p.page_tokens * p.H + h) * D : 0;
+    t_sb0 = t_ok0 ? ((pg0 * p.H + h) * p.page_tokens + static_cast<int>(rip)) * 4 : 0;
+    t_sb1 = t_ok1 ? ((pg1 * p.H + h) * p.page_tokens) * 4 : 0;
   };
-  // Byte offsets of (key t0 + k, head h, d = 0) in a code pool and of its
-  // scale; out of range for keys past n_kv or on invalid pages.
   auto key_offsets = [&](int k, int& code_off, int& scale_off) {
-    int r = tile_rip0 + k;
-    int page = tile_page0;
-    if (r >= p.page_tokens) {
-      r -= p.page_tokens;
-      page = tile_page1;
-    }
-    const bool ok = page >= 0 && tile_t0 + k < p.n_kv;
-    code_off = ok ? ((page * p.page_tokens + r) * p.H + h) * D : kOutOfRange;
-    scale_off = ok ? ((page * p.H + h) * p.page_tokens + r) * 4 : kOutOfRange;
+    const bool first = k < t_split;
+    const bool ok = k < t_valid && (first ? t_ok0 : t_ok1);
+    const int kr = first ? k : k - t_split;
+    code_off = ok ? (first ? t_cb0 : t_cb1) + kr * HD : kOutOfRange;
+    scale_off = ok ? (first ? t_sb0 : t_sb1) + kr * 4 : kOutOfRange;
   };
 
   // ---- per-thread staging of one K/V tile ----------------------------------
   // K: 2 x 16 codes (key = c / 8, d0 = 16 * (c % 8)), c = tid + 256 * i.
   // V: 2 tasks of 4 keys x 4 d (dword loads), task = tid + 256 * i:
   //    key group kg = task / 32 (keys 4kg..4kg+3), d = 4 * (task % 32).
-  // Scales: threads 0..63 load s_k of key tid, 64..127 s_v of key tid - 64.
+  // Each thread also loads the scales of the keys it decodes.
   u32x4 rk_code[PGR][KCH];
   uint32_t rv_code[PGR][VT][4];
-  float rscale[PGR];
+  float rk_s[PGR][KCH];
+  float rv_s[PGR][VT][4];
   // second halves of the dense bf16 variant's staging (unused for FP8 pages)
   u32x4 rk_hi[DENSE ? PGR : 1][DENSE ? KCH : 1];
   uint32_t rv_hi[DENSE ? PGR : 1][DENSE ? VT : 1][4];
@@ -212,7 +223,6 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
           rv_hi[u][i][j] = w2[1];
         }
       }
-      rscale[u] = (t0 + (tid & (BKV - 1)) < p.n_kv) ? 1.0f : 0.0f;
       return;
     }
     map_tile(t0);
@@ -222,6 +232,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
       int co, so;
       key_offsets(c >> 3, co, so);
       rk_code[u][i] = __builtin_amdgcn_raw_buffer_load_b128(rk, co == kOutOfRange ? co : co + (c & 7) * 16, 0, 0);
+      rk_s[u][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsk, so, 0, 0));
     }
 #pragma unroll
     for (int i = 0; i < VT; ++i) {
@@ -232,19 +243,15 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
         int co, so;
         key_offsets(4 * kg + j, co, so);
         rv_code[u][i][j] = __builtin_amdgcn_raw_buffer_load_b32(rv, co == kOutOfRange ? co : co + d0, 0, 0);
+        rv_s[u][i][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsv, so, 0, 0));
       }
     }
-    // threads 0..63 fetch s_k, 64..127 s_v (others fetch a dummy s_v)
-    int co, so;
-    key_offsets(tid & (BKV - 1), co, so);
-    rscale[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tid < BKV ? rsk : rsv, so, 0, 0));
   };
 
   auto store_tile = [&](auto buf, int lbuf) {
     constexpr int u = decltype(buf)::value;
     uint8_t* sk = lds + lbuf * STAGE;
     uint8_t* sv = sk + K_TILE;
-    float* ss = reinterpret_cast<float*>(sv + V_TILE);
     if constexpr (DENSE) {
 #pragma unroll
       for (int i = 0; i < KCH; ++i) {
@@ -268,16 +275,16 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
           *reinterpret_cast<uint2*>(sv + (d0 + j) * VP + pos * 2) = make_uint2(lo, hi);
         }
       }
-      if (tid < 2 * BKV) ss[tid] = tid < BKV ? rscale[u] * p.qk_scale : rscale[u];
       return;
     }
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = tid + THREADS * i;
-      const uint2 a = decode4_bf16(rk_code[u][i][0]);
-      const uint2 b = decode4_bf16(rk_code[u][i][1]);
-      const uint2 e = decode4_bf16(rk_code[u][i][2]);
-      const uint2 f = decode4_bf16(rk_code[u][i][3]);
+      const float ks = rk_s[u][i];
+      const uint2 a = dequant4_bf16(rk_code[u][i][0], ks, ks, ks, ks);
+      const uint2 b = dequant4_bf16(rk_code[u][i][1], ks, ks, ks, ks);
+      const uint2 e = dequant4_bf16(rk_code[u][i][2], ks, ks, ks, ks);
+      const uint2 f = dequant4_bf16(rk_code[u][i][3], ks, ks, ks, ks);
       uint4* dst = reinterpret_cast<uint4*>(sk + (c >> 3) * KP + (c & 7) * 32);
       dst[0] = make_uint4(a.x, a.y, b.x, b.y);
       dst[1] = make_uint4(e.x, e.y, f.x, f.y);
@@ -293,11 +300,10 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
         // byte j of the four key dwords = the codes of d0 + j for keys 4kg..4kg+3
         const uint32_t lo = __builtin_amdgcn_perm(rv_code[u][i][1], rv_code[u][i][0], 0x0c0c0400u + 0x00000101u * j);
         const uint32_t hi = __builtin_amdgcn_perm(rv_code[u][i][3], rv_code[u][i][2], 0x0c0c0400u + 0x00000101u * j);
-        const uint2 dec = decode4_bf16(lo | (hi << 16));
+        const uint2 dec = dequant4_bf16(lo | (hi << 16), rv_s[u][i][0], rv_s[u][i][1], rv_s[u][i][2], rv_s[u][i][3]);
         *reinterpret_cast<uint2*>(sv + (d0 + j) * VP + pos * 2) = dec;
       }
     }
-    if (tid < 2 * BKV) ss[tid] = tid < BKV ? rscale[u] * p.qk_scale : rscale[u];
   };
 
   // ---- Q^T fragments for this wave's 32 queries (kept for the whole kernel)
@@ -337,7 +343,6 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
     load_tile(uu, (it + PGR) * BKV);
     const uint8_t* sk = lds + cur * STAGE;
     const uint8_t* sv = sk + K_TILE;
-    const float* ss = reinterpret_cast<const float*>(sv + V_TILE);
 
     // S^T = K Q^T for 2 blocks of 32 keys
     v16f s[2];
@@ -351,7 +356,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
       }
     }
-    // row (key) scaling by c * s_k, masking of keys past n_kv, tile max
+    // masking of keys past n_kv (last tile only), tile max of the raw scores
     const int key_base = it * BKV;
     const bool partial = key_base + BKV > p.n_kv;
     float mt = -INFINITY;
@@ -360,22 +365,20 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int kk = b * 32 + g * 8 + half * 4;
-        const float4 sc = *reinterpret_cast<const float4*>(ss + kk);
-        const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = s[b][4 * g + e] * scv[e];
-          if (partial && key_base + kk + e >= p.n_kv) v = -INFINITY;
-          s[b][4 * g + e] = v;
-          mt = fmaxf(mt, v);
+          if (partial && key_base + kk + e >= p.n_kv) s[b][4 * g + e] = -INFINITY;
+          mt = fmaxf(mt, s[b][4 * g + e]);
         }
       }
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32));
+    // exponents in base 2: p = 2^(c * (s - m)), c = softmax_scale * log2(e) > 0
+    const float c = p.qk_scale;
     const float m_new = fmaxf(m_run, mt);
-    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(c * (m_run - m_new));
     m_run = m_new;
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float neg_mc = (m_new == -INFINITY) ? 0.f : -m_new * c;
     float lsum = 0.f;
     v8bf pf[4];
 #pragma unroll
@@ -386,15 +389,11 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void attn_paged_fp8_kernel(A
 #pragma unroll
         for (int g2 = 0; g2 < 2; ++g2) {
           const int g = hh * 2 + g2;
-          const int kk = b * 32 + g * 8 + half * 4;
-          const float4 sv4 = *reinterpret_cast<const float4*>(ss + BKV + kk);
-          const float svv[4] = {sv4.x, sv4.y, sv4.z, sv4.w};
           float pv[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float pe = __builtin_amdgcn_exp2f(s[b][4 * g + e] - m_use);
-            lsum += pe;
-            pv[e] = pe * svv[e];
+            pv[e] = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g + e], c, neg_mc));
+            lsum += pv[e];
           }
           pk[2 * g2] = cvt_bf16x2(pv[0], pv[1]);
           pk[2 * g2 + 1] = cvt_bf16x2(pv[2], pv[3]);
