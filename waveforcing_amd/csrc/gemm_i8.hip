@@ -11,21 +11,29 @@
 // scale_b, + bias, bf16 out) and of the FFN's GELU(approximate='tanh')
 // (naive_rt/rolling_forcing/wan/modules/causal_model.py:342-344).
 //
-// Tiling (template parameters; the launcher's choice is measured): a
-// workgroup computes a BM x BN tile with WM x WN waves, each wave a grid of
-// 32x32 v_mfma_i32_32x32x32_i8 blocks; K advances 128 bytes per step.  Both
-// operands are K-contiguous ("NT").  Global -> register staging uses buffer
-// loads (the descriptor range zero-fills rows past M/N, so loads carry no
-// predicate or branch) issued PGR steps ahead; LDS holds two stages with rows
-// padded to 144 B so the 16-byte fragment reads of 8 consecutive rows hit
-// distinct banks; each wave reads the fragments of sub-step s+1 while the
-// MFMAs of sub-step s run.  The weight fragment is the MFMA's first operand
-// and the activation fragment the second, so the 32x32 result block is
-// (n, m): each lane ends up with 4 consecutive output features of one token
-// per accumulator group, stored as one 8-byte bf16 vector.  Tiles are
-// ordered so that the workgroups one XCD receives (blockIdx % 8) form a
-// contiguous range, walked in bands of GROUP_M tile rows, so co-resident
-// workgroups share A and W panels in that XCD's L2.
+// Structure (one 128 x 256 output tile per workgroup of 8 waves, each wave
+// 64 x 64 as 2 x 2 blocks of v_mfma_i32_32x32x32_i8; both operands
+// K-contiguous):
+//  * Global -> LDS by DMA (buffer_load_dwordx4 ... lds): each instruction
+//    moves 1 KB = 8 rows x 128 K-bytes into a contiguous LDS block, no
+//    registers involved.  Lane l lands at byte 16 l, i.e. row l/8, position
+//    l%8; it fetches K chunk (l%8) ^ ((row/2)%8), so LDS holds chunk c of row
+//    r at 16 (c ^ ((r/2)%8)) and the 16-byte fragment reads of 16 consecutive
+//    rows hit 16 distinct bank groups.  The buffer descriptor's range
+//    zero-fills rows past M / N, and K-tail chunks are pointed past it.
+//  * Three LDS stages of 48 KB.  A K step (128 bytes) is four 32-byte
+//    sub-steps; fragments of sub-step g+1 are read while the MFMAs of g
+//    issue, one LDS read or DMA placed after each MFMA.  The workgroup
+//    barrier sits in the last sub-step, after its fragments are in
+//    registers, so that sub-step's MFMAs cover the first reads of the next
+//    stage; the DMA of step j is spread over the last sub-step of step j-3
+//    and the first three of step j-2.
+//  * Epilogue: scales and bias are loaded at kernel start; results are
+//    converted with v_cvt_pk_bf16_f32 (round to nearest even), staged in LDS
+//    and written as row-contiguous 16-byte vectors (full 128-byte lines).
+//  * Tiles are ordered so that the workgroups one XCD receives (blockIdx % 8)
+//    form a contiguous range, walked in bands of 8 tile rows, so co-resident
+//    workgroups share A and W panels in that XCD's L2.
 #include <utility>
 
 #include "launchers.hpp"
@@ -37,22 +45,46 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int BK = 128;
+constexpr int BK = 128;  // K bytes per step
+constexpr int BM = 128, BN = 256, WM = 2, WN = 4;
+constexpr int NW = WM * WN;
+constexpr int THREADS = NW * 64;
+constexpr int MI = BM / WM / 32, NI = BN / WN / 32;  // 32x32 blocks per wave
+constexpr int A_BYTES = BM * BK;
+constexpr int STAGE = (BM + BN) * BK;
+constexpr int ST = 3;
+constexpr int NBA = BM / 8 / NW, NBB = BN / 8 / NW;  // 1 KB DMA blocks per wave and step
+constexpr int NDMA = NBA + NBB;
+constexpr int GROUP_M = 8;
+constexpr int NUM_XCD = 8;
+constexpr int OUT_PITCH = BN * 2 + 16;  // bf16 epilogue tile row pitch (bytes)
+static_assert(NBA * 8 * NW == BM && NBB * 8 * NW == BN, "DMA blocks");
+static_assert(BM * OUT_PITCH <= ST * STAGE, "epilogue tile fits the stages");
 // Word 3 of a raw (untyped, stride 0) buffer resource on gfx9-family parts:
 // DATA_FORMAT = 32 bit.  With it, offsets >= num_records read as zero.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 constexpr int kOutOfRange = 0x7ffffff0;
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-constexpr int PITCH = BK + 16;  // LDS row pitch in bytes
-constexpr int NUM_XCD = 8;
 
-template <int N, typename F, int... I>
+template <typename F, int... I>
 __device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
   (f(std::integral_constant<int, I>{}), ...);
 }
 template <int N, typename F>
 __device__ inline void static_for(F&& f) {
-  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+template <int V>
+using ic = std::integral_constant<int, V>;
+
+// s_waitcnt with vmcnt(VM), lgkmcnt(LGKM) (15 = no wait), expcnt unchanged.
+template <int VM, int LGKM>
+__device__ inline void wait_counts() {
+  static_assert(VM >= 0 && VM < 64 && LGKM >= 0 && LGKM < 16, "wait counts");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | 0x70 | (LGKM << 8));
+}
+
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds_block, int offset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_block, 16, offset, 0, 0, 0);
 }
 
 struct GemmArgs {
@@ -65,231 +97,213 @@ struct GemmArgs {
   int32_t* acc_out;      // [M, N] int32 or null
   int M, N, K;
   int64_t ldy;
+  int vec16;             // y and ldy allow 16-byte row stores
 };
 
+// GELU(approximate='tanh') with tanh(u) = 1 - 2 / (1 + e^{2u}) on the
+// hardware exponential: absolute error ~1e-7 against tanhf.
 __device__ inline float gelu_tanh(float x) {
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
+  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  const float t = 1.0f - 2.0f / (1.0f + __expf(2.0f * u));
+  return 0.5f * x * (1.0f + t);
 }
 
-__device__ inline float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_rne(f)); }
-
-// BM x BN workgroup tile, WM x WN waves, each wave (BM/WM) x (BN/WN) as
-// MI x NI blocks of 32x32.  OCC = waves per SIMD the register budget is
-// sized for (1: one workgroup of 4 waves per CU; 2: two).
-template <int BM, int BN, int WM, int WN, int OCC, int PGR, bool XCD_REMAP, int GROUP_M, bool HAS_BIAS, bool GELU>
-__global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_i8_kernel(GemmArgs p) {
-  constexpr int THREADS = WM * WN * 64;
-  constexpr int A_STAGE = BM * PITCH;
-  constexpr int B_STAGE = BN * PITCH;
-  constexpr int STAGE = A_STAGE + B_STAGE;
-  constexpr int A_CHUNKS = BM * BK / 16 / THREADS;
-  constexpr int B_CHUNKS = BN * BK / 16 / THREADS;
-  constexpr int MI = BM / WM / 32;
-  constexpr int NI = BN / WN / 32;
-  static_assert(A_CHUNKS * 16 * THREADS == BM * BK && B_CHUNKS * 16 * THREADS == BN * BK, "tile/threads");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+template <bool HAS_BIAS, bool GELU>
+__global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[ST * STAGE];
 
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (p.N + BN - 1) / BN;
   const int n_tiles = tiles_m * tiles_n;
-  int t = blockIdx.x;
-  if (XCD_REMAP) {
-    const int per_xcd = (n_tiles + NUM_XCD - 1) / NUM_XCD;
-    t = (blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
-  }
+  const int per_xcd = (n_tiles + NUM_XCD - 1) / NUM_XCD;
+  const int t = (blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
   if (t >= n_tiles) return;
-  int tm = t / tiles_n, tn = t % tiles_n;
-  if (GROUP_M > 0) {
-    // Grouped order: bands of GROUP_M tile rows swept column by column, so
-    // the workgroups resident on one XCD at a time form a compact block and
-    // share A rows and W rows in that XCD's L2.
-    const int per_group = GROUP_M * tiles_n;
-    const int first_m = (t / per_group) * GROUP_M;
-    const int rows = min(tiles_m - first_m, GROUP_M);
-    const int r = t % per_group;
-    tm = first_m + r % rows;
-    tn = r / rows;
-  }
-  const int m0 = tm * BM;
-  const int n0 = tn * BN;
+  // Grouped order: bands of GROUP_M tile rows swept column by column.
+  const int per_group = GROUP_M * tiles_n;
+  const int first_m = (t / per_group) * GROUP_M;
+  const int band = min(tiles_m - first_m, GROUP_M);
+  const int m0 = (first_m + (t % per_group) % band) * BM;
+  const int n0 = ((t % per_group) / band) * BN;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN;
   const int wn = wave % WN;
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
-  // Global -> register staging: PGR register buffers, so the loads of K
-  // step kb + PGR are issued while step kb computes and have PGR compute
-  // steps to arrive.  Buffer indices are compile-time (loop unrolled by PGR).
-  uint4 ra[PGR][A_CHUNKS], rb[PGR][B_CHUNKS];
-  // Buffer loads: the descriptor's range (M*K, N*K bytes) makes the hardware
-  // return zeros for rows past M / N, and K-tail chunks are pointed past the
-  // range, so the loads need no predicate and no branch.
+  // Epilogue operands, loaded now so their latency hides under the K loop.
+  float sxv[MI];
+  float4 swv[NI][4];
+  uint2 bv[NI][4];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) sxv[i] = p.sx[min(m0 + wm * (BM / WM) + i * 32 + l32, p.M - 1)];
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int gn = min(n0 + wn * (BN / WN) + j * 32 + 8 * g + 4 * half, p.N - 4);
+      swv[j][g] = *reinterpret_cast<const float4*>(p.sw + gn);
+      bv[j][g] = HAS_BIAS ? *reinterpret_cast<const uint2*>(p.bias + gn) : make_uint2(0, 0);
+    }
+
   const __amdgpu_buffer_rsrc_t rsrc_a =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), 0, p.M * p.K, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsrc_w =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), 0, p.N * p.K, kBufferRsrcWord3);
-  int off_a[A_CHUNKS], col_a[A_CHUNKS], off_b[B_CHUNKS], col_b[B_CHUNKS];
+
+  // DMA block j of this wave: A rows (j * NW + wave) * 8 .. + 7 for j < NBA,
+  // else W rows ((j - NBA) * NW + wave) * 8 .. + 7.
+  int doff[NDMA], dcol[NDMA];
 #pragma unroll
-  for (int i = 0; i < A_CHUNKS; ++i) {
-    const int c = tid + THREADS * i;
-    col_a[i] = (c & 7) * 16;
-    off_a[i] = (m0 + (c >> 3)) * p.K + col_a[i];
+  for (int j = 0; j < NDMA; ++j) {
+    const bool is_a = j < NBA;
+    const int r = ((is_a ? j : j - NBA) * NW + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    dcol[j] = c * 16;
+    doff[j] = ((is_a ? m0 : n0) + r) * p.K + c * 16;
   }
-#pragma unroll
-  for (int i = 0; i < B_CHUNKS; ++i) {
-    const int c = tid + THREADS * i;
-    col_b[i] = (c & 7) * 16;
-    off_b[i] = (n0 + (c >> 3)) * p.K + col_b[i];
-  }
-  auto load_stage = [&](auto buf, int k0) {
-    constexpr int u = decltype(buf)::value;
-#pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int off = (k0 + col_a[i] < p.K) ? off_a[i] + k0 : kOutOfRange;
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, off, 0, 0);
-      ra[u][i] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-      const int off = (k0 + col_b[i] < p.K) ? off_b[i] + k0 : kOutOfRange;
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, off, 0, 0);
-      rb[u][i] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
-  };
-  auto store_stage = [&](auto buf, int lbuf) {
-    constexpr int u = decltype(buf)::value;
-    uint8_t* sa = lds + lbuf * STAGE;
-    uint8_t* sb = sa + A_STAGE;
-#pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + THREADS * i;
-      *reinterpret_cast<uint4*>(sa + (c >> 3) * PITCH + (c & 7) * 16) = ra[u][i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + THREADS * i;
-      *reinterpret_cast<uint4*>(sb + (c >> 3) * PITCH + (c & 7) * 16) = rb[u][i];
-    }
+  auto dma = [&](auto J, int k0, int stage) {
+    constexpr int j = decltype(J)::value;
+    const int off = (k0 + dcol[j] < p.K) ? doff[j] + k0 : kOutOfRange;
+    if constexpr (j < NBA)
+      dma16(rsrc_a, lds + stage * STAGE + (j * NW + wave) * 1024, off);
+    else
+      dma16(rsrc_w, lds + stage * STAGE + A_BYTES + ((j - NBA) * NW + wave) * 1024, off);
   };
 
-  v16i acc[NI][MI];  // [n block j][m block i]
+  // Fragment reads: row R, K chunk c at R*128 + 16*(c ^ ((R/2)%8)).  The rows
+  // one lane reads differ by multiples of 32, so the swizzle is per lane.
+  const int x = (l32 >> 1) & 7;
+  const int lane_a = (wm * (BM / WM) + l32) * BK + 16 * (half ^ (x & 1));
+  const int lane_b = A_BYTES + (wn * (BN / WN) + l32) * BK + 16 * (half ^ (x & 1));
+  int sub_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) sub_off[s] = 32 * (s ^ (x >> 1));
+
+  v16i acc[NI][MI];
 #pragma unroll
   for (int j = 0; j < NI; ++j)
 #pragma unroll
     for (int i = 0; i < MI; ++i) acc[j][i] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  v4i fa[2][MI], fw[2][NI];
 
-  auto compute = [&](int lbuf) {
-    const uint8_t* sa = lds + lbuf * STAGE + (wm * (BM / WM) + l32) * PITCH + half * 16;
-    const uint8_t* sb = lds + lbuf * STAGE + A_STAGE + (wn * (BN / WN) + l32) * PITCH + half * 16;
-    // Fragments of sub-step s + 1 are read while the MFMAs of sub-step s run.
-    v4i fa[2][MI], fw[2][NI];
-#pragma unroll
-    for (int i = 0; i < MI; ++i) fa[0][i] = *reinterpret_cast<const v4i*>(sa + i * 32 * PITCH);
-#pragma unroll
-    for (int j = 0; j < NI; ++j) fw[0][j] = *reinterpret_cast<const v4i*>(sb + j * 32 * PITCH);
-#pragma unroll
-    for (int s = 0; s < BK / 32; ++s) {
-      const int cb = s & 1;
-      if (s + 1 < BK / 32) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-          fa[cb ^ 1][i] = *reinterpret_cast<const v4i*>(sa + i * 32 * PITCH + (s + 1) * 32);
-#pragma unroll
-        for (int j = 0; j < NI; ++j)
-          fw[cb ^ 1][j] = *reinterpret_cast<const v4i*>(sb + j * 32 * PITCH + (s + 1) * 32);
-      }
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[cb][j], fa[cb][i], acc[j][i], 0, 0, 0);
-    }
+  // Fragment read q (A blocks first, then W blocks) of sub-step s into buffer B.
+  auto frag_read = [&](auto Q, auto B, int stage, int s) {
+    constexpr int q = decltype(Q)::value;
+    constexpr int b = decltype(B)::value;
+    if constexpr (q < MI)
+      fa[b][q] = *reinterpret_cast<const v4i*>(lds + stage * STAGE + lane_a + sub_off[s] + q * 32 * BK);
+    else
+      fw[b][q - MI] = *reinterpret_cast<const v4i*>(lds + stage * STAGE + lane_b + sub_off[s] + (q - MI) * 32 * BK);
+  };
+  // The MFMAs of buffer B, each followed by one of: a read of sub-step rs of
+  // rstage into buffer 1-B, or a DMA of slot SLOT (quarter of a step's DMAs)
+  // for the step at K offset dk0 into dstage.
+  auto substep = [&](auto B, int rstage, int rs, auto SLOT, int dk0, int dstage) {
+    constexpr int b = decltype(B)::value;
+    constexpr int slot = decltype(SLOT)::value;
+    constexpr int d_lo = (slot * NDMA + 3) / 4;
+    constexpr int d_hi = ((slot + 1) * NDMA + 3) / 4;
+    constexpr int nd = d_hi - d_lo;
+    constexpr int NMF = MI * NI, NRD = MI + NI;
+    static_assert(nd <= NMF && NRD <= NMF, "interleave");
+    static_for<NMF>([&](auto Q) {
+      constexpr int q = decltype(Q)::value;
+      constexpr int jj = q / MI, ii = q % MI;
+      acc[jj][ii] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[b][jj], fa[b][ii], acc[jj][ii], 0, 0, 0);
+      if constexpr (q < NRD) frag_read(ic<q>{}, ic<b ^ 1>{}, rstage, rs);
+      if constexpr (q >= NMF - nd) dma(ic<d_lo + q - (NMF - nd)>{}, dk0, dstage);
+      __builtin_amdgcn_sched_barrier(0);
+    });
   };
 
-  // Steps past K load zeros (a zero contribution), so the step count is
-  // padded to a multiple of PGR and every step runs unconditionally.
-  const int nk = ((p.K + BK - 1) / BK + PGR - 1) / PGR * PGR;
-  static_for<PGR>([&](auto u) { load_stage(u, u.value * BK); });
-  store_stage(std::integral_constant<int, 0>{}, 0);
-  __syncthreads();
+  // Steps past K load zeros (a zero contribution): every step runs the same
+  // code, and the last DMAs (of steps nk .. nk+2) only fill unused stages.
+  const int nk = (p.K + BK - 1) / BK;
+  static_for<NDMA>([&](auto J) { dma(J, 0, 0); });
+  static_for<NDMA>([&](auto J) { dma(J, BK, 1); });
+  wait_counts<NDMA, 0>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  static_for<(NDMA + 3) / 4>([&](auto J) { dma(J, 2 * BK, 2); });
+  static_for<MI + NI>([&](auto Q) { frag_read(Q, ic<0>{}, 0, 0); });
+  __builtin_amdgcn_sched_barrier(0);
 
-  for (int kb0 = 0; kb0 < nk; kb0 += PGR) {
-    static_for<PGR>([&](auto u) {
-      constexpr int U = decltype(u)::value;
-      const int kb = kb0 + U;
-      // register buffer U held step kb, already in LDS: refill it with step kb + PGR
-      load_stage(u, (kb + PGR) * BK);
-      compute(kb & 1);
-      store_stage(std::integral_constant<int, (U + 1) % PGR>{}, (kb + 1) & 1);
-      __syncthreads();
-    });
+  int c0 = 0, c1 = 1, c2 = 2;  // stages of steps kb, kb+1, kb+2
+  for (int kb = 0; kb < nk; ++kb) {
+    const int k2 = (kb + 2) * BK;
+    substep(ic<0>{}, c0, 1, ic<1>{}, k2, c2);
+    substep(ic<1>{}, c0, 2, ic<2>{}, k2, c2);
+    substep(ic<0>{}, c0, 3, ic<3>{}, k2, c2);
+    // Own reads of this stage done, own DMAs of step kb+1 landed (only step
+    // kb+2's may still be in flight); the barrier makes that hold for every wave.
+    wait_counts<NDMA, 0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    substep(ic<1>{}, c1, 0, ic<0>{}, (kb + 3) * BK, c0);
+    const int c = c0;
+    c0 = c1;
+    c1 = c2;
+    c2 = c;
   }
+  // All DMAs landed and all waves past their last LDS read before the
+  // stages are reused for the output tile.
+  wait_counts<0, 0>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 
-  // Epilogue.  Block (j, i) element (n, m): m = l32, n = 8*(r/4) + 4*half + r%4.
+  // Block (j, i) element (n, m): m = l32, n = 8*(r/4) + 4*half + r%4.
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
-    const int gm = m0 + wm * (BM / WM) + i * 32 + l32;
-    const bool row_ok = gm < p.M;
-    const float sxm = row_ok ? p.sx[gm] : 0.f;
+    const int r = wm * (BM / WM) + i * 32 + l32;
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
+    for (int j = 0; j < NI; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int gn = n0 + wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
-        // N % 4 == 0 (checked at the entry point): a 4-wide group is all in or all out.
-        if (row_ok && gn < p.N) {
-          const int a0 = acc[j][i][4 * g + 0], a1 = acc[j][i][4 * g + 1];
-          const int a2 = acc[j][i][4 * g + 2], a3 = acc[j][i][4 * g + 3];
-          const float4 swv = *reinterpret_cast<const float4*>(p.sw + gn);
-          float y0 = __fmul_rn(__fmul_rn(static_cast<float>(a0), sxm), swv.x);
-          float y1 = __fmul_rn(__fmul_rn(static_cast<float>(a1), sxm), swv.y);
-          float y2 = __fmul_rn(__fmul_rn(static_cast<float>(a2), sxm), swv.z);
-          float y3 = __fmul_rn(__fmul_rn(static_cast<float>(a3), sxm), swv.w);
-          if (HAS_BIAS) {
-            const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + gn);
-            y0 = __fadd_rn(y0, bf16_lo_to_f32(bb.x));
-            y1 = __fadd_rn(y1, bf16_hi_to_f32(bb.x));
-            y2 = __fadd_rn(y2, bf16_lo_to_f32(bb.y));
-            y3 = __fadd_rn(y3, bf16_hi_to_f32(bb.y));
-          }
-          if (GELU) {
-            y0 = gelu_tanh(round_bf16(y0));
-            y1 = gelu_tanh(round_bf16(y1));
-            y2 = gelu_tanh(round_bf16(y2));
-            y3 = gelu_tanh(round_bf16(y3));
-          }
-          const uint2 packed = make_uint2(
-              static_cast<uint32_t>(f32_to_bf16_rne(y0)) | (static_cast<uint32_t>(f32_to_bf16_rne(y1)) << 16),
-              static_cast<uint32_t>(f32_to_bf16_rne(y2)) | (static_cast<uint32_t>(f32_to_bf16_rne(y3)) << 16));
-          *reinterpret_cast<uint2*>(p.y + static_cast<int64_t>(gm) * p.ldy + gn) = packed;
-          if (p.acc_out)
-            *reinterpret_cast<int4*>(p.acc_out + static_cast<int64_t>(gm) * p.N + gn) = make_int4(a0, a1, a2, a3);
+        const int c = wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
+        float y[4];
+        const float sw4[4] = {swv[j][g].x, swv[j][g].y, swv[j][g].z, swv[j][g].w};
+        const uint32_t bb[4] = {bv[j][g].x << 16, bv[j][g].x & 0xffff0000u, bv[j][g].y << 16,
+                                bv[j][g].y & 0xffff0000u};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y[e] = __fmul_rn(__fmul_rn(static_cast<float>(acc[j][i][4 * g + e]), sxv[i]), sw4[e]);
+          if (HAS_BIAS) y[e] = __fadd_rn(y[e], __uint_as_float(bb[e]));
+          if (GELU) y[e] = gelu_tanh(__uint_as_float(pack_bf16x2_hw(y[e], 0.f) << 16));
         }
+        *reinterpret_cast<uint2*>(lds + r * OUT_PITCH + c * 2) =
+            make_uint2(pack_bf16x2_hw(y[0], y[1]), pack_bf16x2_hw(y[2], y[3]));
+        if (p.acc_out) {
+          const int gm = m0 + r, gn = n0 + c;
+          if (gm < p.M && gn < p.N)
+            *reinterpret_cast<int4*>(p.acc_out + static_cast<int64_t>(gm) * p.N + gn) =
+                make_int4(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
+        }
+      }
+  }
+  __syncthreads();
+  constexpr int CPR = BN * 2 / 16;  // 16-byte chunks per tile row
+  constexpr int ITERS = BM * CPR / THREADS;
+  static_assert(ITERS * THREADS == BM * CPR, "epilogue chunks");
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int id = it * THREADS + static_cast<int>(threadIdx.x);
+    const int r = id / CPR, c = id % CPR;
+    const int gm = m0 + r, gn = n0 + c * 8;
+    const uint4 v = *reinterpret_cast<const uint4*>(lds + r * OUT_PITCH + c * 16);
+    if (gm < p.M && gn < p.N) {
+      uint16_t* dst = p.y + static_cast<int64_t>(gm) * p.ldy + gn;
+      if (p.vec16 && gn + 8 <= p.N) {
+        *reinterpret_cast<uint4*>(dst) = v;
+      } else {
+        // N % 4 == 0 (checked at the entry point): the first 4 columns are in.
+        *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
+        if (gn + 8 <= p.N) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
       }
     }
   }
-}
-
-template <int BM, int BN, int WM, int WN, int OCC, int PGR, bool XCD_REMAP, int GROUP_M>
-int launch_cfg(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream) {
-  const int64_t tiles = ((static_cast<int64_t>(p.M) + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  const int64_t grid = XCD_REMAP ? (tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD : tiles;
-  const dim3 g(static_cast<uint32_t>(grid)), b(WM * WN * 64);
-  if (bias && gelu)
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, OCC, PGR, XCD_REMAP, GROUP_M, true, true>), g, b, 0, stream, p);
-  else if (bias)
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, OCC, PGR, XCD_REMAP, GROUP_M, true, false>), g, b, 0, stream, p);
-  else if (gelu)
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, OCC, PGR, XCD_REMAP, GROUP_M, false, true>), g, b, 0, stream, p);
-  else
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WM, WN, OCC, PGR, XCD_REMAP, GROUP_M, false, false>), g, b, 0, stream, p);
-  return check_launch("wf_gemm_i8");
 }
 
 GemmArgs make_args(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64_t K, const float* sx,
@@ -306,6 +320,7 @@ GemmArgs make_args(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64
   p.N = static_cast<int>(N);
   p.K = static_cast<int>(K);
   p.ldy = ldy;
+  p.vec16 = (ldy % 8 == 0) && ((reinterpret_cast<uintptr_t>(y) & 15u) == 0);
   return p;
 }
 
@@ -315,11 +330,17 @@ int launch_gemm_i8(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64
                    const float* sw, const void* bias, void* y, int64_t ldy, int32_t* acc_out, int gelu,
                    hipStream_t stream) {
   const GemmArgs p = make_args(a, w, M, N, K, sx, sw, bias, y, ldy, acc_out);
-  // 128 x 256 tiles, 2 x 4 waves of 64 x 64, two workgroups per CU, loads
-  // two K steps ahead, XCD-contiguous grouped order (bands of 8 tile rows):
-  // the best of a sweep over tile shape, waves, occupancy, prefetch depth and
-  // rasterization on the Wan-1.3B/14B linear shapes.
-  return launch_cfg<128, 256, 2, 4, 2, 2, true, 8>(p, bias != nullptr, gelu != 0, stream);
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD)), block(THREADS);
+  if (bias && gelu)
+    hipLaunchKernelGGL((gemm_i8_kernel<true, true>), grid, block, 0, stream, p);
+  else if (bias)
+    hipLaunchKernelGGL((gemm_i8_kernel<true, false>), grid, block, 0, stream, p);
+  else if (gelu)
+    hipLaunchKernelGGL((gemm_i8_kernel<false, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm_i8_kernel<false, false>), grid, block, 0, stream, p);
+  return check_launch("wf_gemm_i8");
 }
 
 }  // namespace wf

@@ -75,6 +75,15 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
          (static_cast<uint32_t>(f32_to_bf16_rne(b)) << 16);
 }
 
+// The same conversion in one instruction (v_cvt_pk_bf16_f32, round to
+// nearest even; equal to pack_bf16x2 for every non-NaN input).
+__device__ inline uint32_t pack_bf16x2_hw(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const f2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
+}
+
 // ------------------------------------------------------- wave64 reductions
 // DPP controls (gfx9): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
 // row_half_mirror (lane i <-> 7-i within 8) = 0x141.
