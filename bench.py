@@ -37,6 +37,7 @@ from waveforcing_amd.kv import Fp8PagePool  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
 LAYERS, TOKENS, HEADS, HEAD_DIM, PAGE = 30, 4680, 12, 128, 1560
 
@@ -120,8 +121,9 @@ def bench_kv(steps: int, warmup: int, dev: str, which=("pack", "unpack", "pack_l
 
 
 def bench_gemm(steps: int, warmup: int, dev: str):
-    """W8A8 int8 linear at the Wan-1.3B shape: GEMM kernel alone and quant + GEMM."""
-    from waveforcing_amd.fp8 import WaveW8A8Linear, _quant_rows_i8, gemm_i8
+    """W8A8 linear at the Wan-1.3B shape: the int8 GEMM alone, quant + GEMM, and the
+    reference's per-tensor e4m3 GEMM alone and with its activation quantization."""
+    from waveforcing_amd.fp8 import WaveFp8Linear, WaveW8A8Linear, _quant_rows_i8, gemm_fp8_pertensor, gemm_i8
 
     x, w, b = inputs.linear_1p3b()
     x, w, b = x.to(dev), w.to(dev), b.to(dev)
@@ -132,19 +134,56 @@ def bench_gemm(steps: int, warmup: int, dev: str):
     ms_gemm = _timed(lambda: [gemm_i8(qx, lin.w_i8, sx, lin.w_scale, lin.bias, out=y) for _ in range(reps)],
                      steps, warmup) / reps
     ms_lin = _timed(lambda: [lin(x) for _ in range(reps)], steps, warmup) / reps
+    f8 = WaveFp8Linear(w, b)
+    from waveforcing_amd import _lib
+    from waveforcing_amd.fp8 import fp8_quant_pertensor
+
+    xc, xs = fp8_quant_pertensor(x, _lib.FP8_TENSOR_ACT)
+    ms_f8 = _timed(lambda: [gemm_fp8_pertensor(xc, f8.w_fp8, xs, f8.w_scale, f8.bias, out=y) for _ in range(reps)],
+                   steps, warmup) / reps
+    ms_f8_lin = _timed(lambda: [f8(x) for _ in range(reps)], steps, warmup) / reps
     M, K = x.shape
     N = w.shape[0]
     ops = 2.0 * M * N * K
     return {"ms_gemm": ms_gemm, "ms_linear": ms_lin, "ops": ops,
-            "tops_gemm": ops / (ms_gemm * 1e-3) / 1e12, "tops_linear": ops / (ms_lin * 1e-3) / 1e12}
+            "tops_gemm": ops / (ms_gemm * 1e-3) / 1e12, "tops_linear": ops / (ms_lin * 1e-3) / 1e12,
+            "ms_fp8_gemm": ms_f8, "tops_fp8_gemm": ops / (ms_f8 * 1e-3) / 1e12,
+            "ms_fp8_linear": ms_f8_lin, "tops_fp8_linear": ops / (ms_f8_lin * 1e-3) / 1e12}
 
 
-def bench_attention(steps: int, warmup: int, dev: str):
-    """Paged FP8 attention: Q [4680, 12, 128] over 8 chunks (37440 keys) of FP8 pages."""
+def bench_block_linears(steps: int, warmup: int, dev: str):
+    """The Wan-1.3B block's W8A8 GEMMs on one 4680-token chunk: fused QKV [4608, 1536], O
+    [1536, 1536], fc_in [8960, 1536] with GELU-tanh, fc_out [1536, 8960] (activations
+    pre-quantized; 345.97 G int8 ops per step)."""
+    from waveforcing_amd.fp8 import _quant_rows_i8, gemm_i8
+
+    M = TOKENS
+    shapes = [(4608, 1536, False), (1536, 1536, False), (8960, 1536, True), (1536, 8960, False)]
+    ops = 0.0
+    calls = []
+    for i, (N, K, gelu) in enumerate(shapes):
+        x = inputs.outlier_activations(M, K, seed=20 + i, chan_seed=30 + i).to(dev)
+        w, b = inputs.linear_weights(N, K, w_seed=40 + i, b_seed=50 + i)
+        qx, sx = _quant_rows_i8(x)
+        qw, sw = _quant_rows_i8(w.to(dev))
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        calls.append((qx, qw, sx, sw, b.to(dev), gelu, y))
+        ops += 2.0 * M * N * K
+
+    def step():
+        for qx, qw, sx, sw, b, gelu, y in calls:
+            gemm_i8(qx, qw, sx, sw, b, gelu=gelu, out=y)
+
+    ms = _timed(step, steps, warmup)
+    return {"ms": ms, "ops": ops, "tops": ops / (ms * 1e-3) / 1e12}
+
+
+def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8):
+    """Paged FP8 attention: Q [4680, 12, 128] over `chunks` chunks (4680 keys each) of FP8 pages."""
     from waveforcing_amd.backend import attn_paged_fp8
     from waveforcing_amd.kv import PagedKV
 
-    H, chunks = HEADS, 8
+    H = HEADS
     n_kv = TOKENS * chunks
     pages = n_kv // PAGE
     pool = Fp8PagePool(2 * pages, H, HEAD_DIM, PAGE, dev)
@@ -159,7 +198,7 @@ def bench_attention(steps: int, warmup: int, dev: str):
     out = torch.empty_like(q)
     ms = _timed(lambda: attn_paged_fp8(q, ctx, out=out), steps, warmup)
     flops = 4.0 * TOKENS * n_kv * H * HEAD_DIM
-    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops, "keys": n_kv}
 
 
 def bench_block(scale: str, steps: int, warmup: int, dev: str):
@@ -248,8 +287,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "attention", "block_1p3b", "block_14b",
-                                       "copy"],
+    ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention",
+                                       "block_1p3b", "block_14b", "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -262,14 +301,17 @@ def main() -> None:
     dev = "cuda:0"
     if args.only:
         fn = {"kv": bench_kv, "kv_pack": lambda s, w, d: bench_kv(s, w, d, ("pack",)),
-              "kv_unpack": lambda s, w, d: bench_kv(s, w, d, ("unpack",)), "gemm": bench_gemm, "attention": bench_attention, "copy": bench_copy,
+              "kv_unpack": lambda s, w, d: bench_kv(s, w, d, ("unpack",)), "gemm": bench_gemm,
+              "linears_1p3b": bench_block_linears, "attention": bench_attention, "copy": bench_copy,
               "block_1p3b": lambda s, w, d: bench_block("1.3b", s, w, d),
               "block_14b": lambda s, w, d: bench_block("14b", s, w, d)}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
     kv = bench_kv(args.steps, args.warmup, dev)
     gm = bench_gemm(max(5, args.steps // 5), 2, dev)
-    at = bench_attention(max(5, args.steps // 5), 2, dev)
+    lin = bench_block_linears(max(5, args.steps // 5), 2, dev)
+    at_sweep = {c: bench_attention(max(5, args.steps // 5), 2, dev, chunks=c) for c in (1, 2, 4, 8)}
+    at = at_sweep[8]
     b13 = bench_block("1.3b", max(5, args.steps // 5), 2, dev)
     b14 = bench_block("14b", max(3, args.steps // 10), 1, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
@@ -316,10 +358,26 @@ def main() -> None:
             "w8a8_linear_tops_incl_act_quant": round(gm["tops_linear"], 1),
             "w8a8_linear_us_incl_act_quant": round(gm["ms_linear"] * 1e3, 2),
             "w8a8_shape": "x[4680,1536] . W[1536,1536]^T int8, per-token/per-channel scales, bias, bf16 out",
+            "fp8_pertensor_gemm_tops": round(gm["tops_fp8_gemm"], 1),
+            "fp8_pertensor_gemm_us": round(gm["ms_fp8_gemm"] * 1e3, 2),
+            "fp8_pertensor_gemm_roofline": {"bound": "mfma", "achieved": round(gm["tops_fp8_gemm"], 1),
+                                            "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                            "frac": round(gm["tops_fp8_gemm"] / FP8_PEAK_TFLOPS, 4)},
+            "fp8_pertensor_linear_us_incl_act_quant": round(gm["ms_fp8_linear"] * 1e3, 2),
+            "fp8_pertensor_shape": "the same linear as WaveFp8Linear: e4m3 per-tensor scales (activation scale in "
+                                   "bf16 arithmetic), fp32 accumulation, bias, bf16 out",
+            "w8a8_block_linears_1p3b_tops": round(lin["tops"], 1),
+            "w8a8_block_linears_1p3b_us": round(lin["ms"] * 1e3, 2),
+            "w8a8_block_linears_1p3b_frac": round(lin["tops"] / INT8_PEAK_TOPS, 4),
+            "w8a8_block_linears_shape": "QKV 4608x1536, O 1536x1536, fc_in 8960x1536 (+GELU), fc_out 1536x8960 on "
+                                        "4680 tokens; 345.97 G int8 ops",
             "attn_paged_fp8_ms": round(at["ms"], 4),
             "attn_paged_fp8_roofline": {"bound": "mfma", "achieved": round(at["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
                                         "unit": "TFLOP/s", "frac": round(at["tflops"] / BF16_PEAK_TFLOPS, 4)},
             "attn_shape": "Q[4680,12,128] bf16 over 37440 keys (8 chunks) of FP8 e4m3fn pages, bf16 MFMA",
+            "attn_paged_fp8_context_sweep": {f"{c}_chunks": {"keys": r["keys"], "ms": round(r["ms"], 4),
+                                                              "tflops": round(r["tflops"], 1)}
+                                             for c, r in at_sweep.items()},
             "dit_block_1p3b_ms_per_chunk": round(b13["ms"], 4),
             "dit_block_14b_ms_per_chunk": round(b14["ms"], 4),
             "dit_block_note": "one block, 4680-token 3-frame chunk, 37440-key FP8 paged self-attn context, "

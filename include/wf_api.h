@@ -6,6 +6,7 @@
  *     gather-dequant of those pages;
  *   - per-token int8 activation quantization and the W8A8 int8 GEMM
  *     (i8 MFMA, int32 accumulation, per-channel dequant + bias, bf16 out);
+ *   - the reference's own per-tensor e4m3 W8A8 linear (FP8 MFMA);
  *   - block-causal attention over the FP8 paged context.
  *
  * Conventions (all entry points):
@@ -113,8 +114,8 @@ int wf_fp8_kv_unpack(const uint8_t* k_codes, const uint8_t* v_codes,
  * weights (rows = output channels).  k % 16 == 0; x, q 16-byte aligned.
  * Replaces the activation/weight quantization of WaveFp8Linear
  * (wave_rt/runtime/fp8.py:33-35 weights, :47-48 activations). */
-int wf_quant_rows_i8(const void* x, int64_t m, int64_t k, int64_t ldx,
-                     int8_t* q, float* scales, void* stream);
+int wf_act_quant_i8(const void* x, int64_t m, int64_t k, int64_t ldx,
+                    int8_t* q, float* scales, void* stream);
 
 #define WF_GEMM_GELU_TANH 1
 
@@ -132,7 +133,7 @@ int wf_gemm_i8(const int8_t* a, const int8_t* w, int64_t m, int64_t n,
                void* y, int64_t ldy, int32_t* acc_out, int32_t flags,
                void* stream);
 
-/* Fused W8A8 linear: wf_quant_rows_i8 of x into the caller's workspace
+/* Fused W8A8 linear: wf_act_quant_i8 of x into the caller's workspace
  * (ws_q int8 [m][k], ws_sx fp32 [m]) followed by wf_gemm_i8 against the
  * pre-quantized weight (qw int8 [n][k], sw fp32 [n]).  The call contract of
  * WaveFp8Linear.forward (wave_rt/runtime/fp8.py:58-61) on 2-D input. */
@@ -140,6 +141,50 @@ int wf_w8a8_linear(const void* x, int64_t m, int64_t k, int64_t ldx,
                    const int8_t* qw, const float* sw, const void* bias,
                    int64_t n, void* y, int64_t ldy, int32_t flags,
                    int8_t* ws_q, float* ws_sx, void* stream);
+
+/* ------------------------------------------------- W8A8 e4m3, per tensor
+ *
+ * The reference's WaveFp8Linear arithmetic (wave_rt/runtime/fp8.py:21-61):
+ * one fp32 scale per weight tensor and one per activation tensor, e4m3fn
+ * codes, fp32 accumulation.
+ */
+
+#define WF_FP8_TENSOR_WEIGHT 0   /* fp32 arithmetic (fp8.py:33-35) */
+#define WF_FP8_TENSOR_ACT 1      /* bf16 tensor arithmetic (fp8.py:47-48) */
+#define WF_FP8_AMAX_PARTIALS 1024 /* floats of the ws_partials workspace */
+
+/* Per-tensor e4m3 quantization of bf16 x [rows][k] (row stride ldx):
+ *   WF_FP8_TENSOR_WEIGHT: s = max(amax|x| / 448, 1e-8) in fp32,
+ *                         codes = e4m3(fp32(x) / s);
+ *   WF_FP8_TENSOR_ACT:    s = max(bf16(amax|x| / 448), bf16(1e-8)),
+ *                         codes = e4m3(bf16(x / s)).
+ * codes are dense u8 [rows][k]; *scale (device fp32) receives s.  ws_partials
+ * holds WF_FP8_AMAX_PARTIALS floats of scratch.  rows > 0, k % 8 == 0.
+ * Replaces WaveFp8Linear.__init__'s weight quantization (fp8.py:33-35) and
+ * the activation quantization of WaveFp8Linear._raw (fp8.py:47-48). */
+int wf_fp8_quant_pertensor(const void* x, int64_t rows, int64_t k,
+                           int64_t ldx, int32_t mode, uint8_t* codes,
+                           float* scale, float* ws_partials, void* stream);
+
+/* e4m3 GEMM y[m][n] = bf16(acc * (a_scale * w_scale) + bias[n]) with
+ * acc = sum_k e4m3(a[m,k]) * e4m3(w[n,k]) in fp32; a_scale and w_scale point
+ * to one device fp32 each; bias bf16 [n] or NULL; y row stride ldy.
+ * k % 16 == 0, n % 4 == 0, ldy % 4 == 0.  Replaces torch._scaled_mm in
+ * WaveFp8Linear._raw (fp8.py:49-56). */
+int wf_gemm_fp8_pertensor(const uint8_t* a, const uint8_t* w, int64_t m,
+                          int64_t n, int64_t k, const float* a_scale,
+                          const float* w_scale, const void* bias, void* y,
+                          int64_t ldy, void* stream);
+
+/* The whole reference linear on 2-D input: wf_fp8_quant_pertensor(x, ACT)
+ * into the caller's workspace (ws_codes u8 [m][k], ws_scale fp32 [1],
+ * ws_partials) followed by wf_gemm_fp8_pertensor against the weight codes
+ * and scale from WF_FP8_TENSOR_WEIGHT.  WaveFp8Linear._raw, fp8.py:46-56. */
+int wf_fp8_linear_pertensor(const void* x, int64_t m, int64_t k, int64_t ldx,
+                            const uint8_t* w_codes, const float* w_scale,
+                            const void* bias, int64_t n, void* y, int64_t ldy,
+                            uint8_t* ws_codes, float* ws_scale,
+                            float* ws_partials, void* stream);
 
 /* ------------------------------------------------------------- attention */
 
@@ -178,7 +223,7 @@ int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads,
  * bf16), then, if given, the bf16 modulation y = bf16(bf16(y * bf16(1 +
  * scale[f])) + shift[f]) with f = row / frame_tokens (scale/shift bf16
  * [frames][dim]); writes y (bf16, row stride ldo) if out != NULL and its
- * per-token int8 quantization (as wf_quant_rows_i8) if q != NULL.
+ * per-token int8 quantization (as wf_act_quant_i8) if q != NULL.
  * dim % 8 == 0, dim <= 5120.  Replaces norm1/norm2 + modulation
  * (naive_rt/rolling_forcing/wan/modules/causal_model.py:381,393-394) and
  * norm3 (:390, model.py:89-99) feeding the W8A8 linears. */

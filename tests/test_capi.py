@@ -55,3 +55,14 @@ def test_last_error_is_thread_local_text():
     with pytest.raises(RuntimeError):
         _lib.call("wf_fp8_e4m3_encode_f32", 0, 0, -5, None)
     assert "n=-5" in _lib.last_error()
+
+
+def test_fp8_pertensor_argument_errors():
+    with pytest.raises(RuntimeError, match="unknown mode"):
+        _lib.call("wf_fp8_quant_pertensor", 16, 4, 64, 64, 7, 32, 48, 64, None)
+    with pytest.raises(RuntimeError, match="empty tensor"):
+        _lib.call("wf_fp8_quant_pertensor", 16, 0, 64, 64, 0, 32, 48, 64, None)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        _lib.call("wf_gemm_fp8_pertensor", 16, 32, 4, 4, 24, 48, 64, None, 80, 4, None)
+    with pytest.raises(RuntimeError, match="null pointer"):
+        _lib.call("wf_fp8_linear_pertensor", 16, 4, 32, 32, 48, 64, None, 8, 80, 8, 96, None, 112, None)

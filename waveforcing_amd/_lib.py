@@ -39,7 +39,7 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _c_void_p,
         _c_void_p,
     ],
-    "wf_quant_rows_i8": [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p],
+    "wf_act_quant_i8": [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p],
     "wf_gemm_i8": [
         _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
         _c_void_p, _i64, _c_void_p, _i32, _c_void_p,
@@ -47,6 +47,14 @@ SIGNATURES: dict[str, list] = {
     "wf_w8a8_linear": [
         _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
         _i64, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
+    ],
+    "wf_fp8_quant_pertensor": [_c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "wf_gemm_fp8_pertensor": [
+        _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
+    ],
+    "wf_fp8_linear_pertensor": [
+        _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,
     ],
     "wf_attn_paged_fp8": [
         _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
@@ -66,6 +74,9 @@ SIGNATURES: dict[str, list] = {
 }
 
 GEMM_GELU_TANH = 1
+FP8_TENSOR_WEIGHT = 0
+FP8_TENSOR_ACT = 1
+FP8_AMAX_PARTIALS = 1024
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

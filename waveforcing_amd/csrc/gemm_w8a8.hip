@@ -1,19 +1,23 @@
-// W8A8 int8 GEMM on the gfx950 i8 matrix cores with a fused dequant + bias
-// (+ optional GELU-tanh) bf16 epilogue.
+// W8A8 GEMMs on the gfx950 matrix cores with fused dequant + bias epilogues.
 //
+// int8 (per-token / per-channel scales):
 //   acc[m,n] = sum_k qx[m,k] * qw[n,k]                      (int32, exact)
 //   y[m,n]   = bf16( (float(acc) * sx[m]) * sw[n] + bias[n] )  (fp32, this order,
 //                                                             no fused multiply-add)
 //   gelu:      y = bf16( gelu_tanh(float(y)) )
+// the per-token / per-channel int8 counterpart of the reference's W8A8 linear
+// (wave_rt/runtime/fp8.py:46-56) with the FFN's GELU(approximate='tanh')
+// folded in (naive_rt/rolling_forcing/wan/modules/causal_model.py:342-344).
 //
-// This is the per-token / per-channel int8 counterpart of the reference's
-// W8A8 linear (wave_rt/runtime/fp8.py:46-56: quantized GEMM, x scale_a x
-// scale_b, + bias, bf16 out) and of the FFN's GELU(approximate='tanh')
-// (naive_rt/rolling_forcing/wan/modules/causal_model.py:342-344).
+// e4m3 (per-tensor scales, the reference's own mode):
+//   acc[m,n] = sum_k e4m3(a[m,k]) * e4m3(w[n,k])            (fp32)
+//   y[m,n]   = bf16( acc * (s_a * s_w) + bias[n] )
+// torch._scaled_mm(x_fp8, w_fp8.t(), scale_a, scale_b, bias, bf16) at
+// wave_rt/runtime/fp8.py:49-56.
 //
 // Structure (one 128 x 256 output tile per workgroup of 8 waves, each wave
-// 64 x 64 as 2 x 2 blocks of v_mfma_i32_32x32x32_i8; both operands
-// K-contiguous):
+// 64 x 64 as 2 x 2 blocks of 32 x 32 MFMAs: v_mfma_i32_32x32x32_i8, or
+// v_mfma_f32_32x32x64_f8f6f4 with e4m3 operands; both operands K-contiguous):
 //  * Global -> LDS by DMA (buffer_load_dwordx4 ... lds): each instruction
 //    moves 1 KB = 8 rows x 128 K-bytes into a contiguous LDS block, no
 //    registers involved.  Lane l lands at byte 16 l, i.e. row l/8, position
@@ -21,19 +25,23 @@
 //    r at 16 (c ^ ((r/2)%8)) and the 16-byte fragment reads of 16 consecutive
 //    rows hit 16 distinct bank groups.  The buffer descriptor's range
 //    zero-fills rows past M / N, and K-tail chunks are pointed past it.
-//  * Three LDS stages of 48 KB.  A K step (128 bytes) is four 32-byte
-//    sub-steps; fragments of sub-step g+1 are read while the MFMAs of g
-//    issue, one LDS read or DMA placed after each MFMA.  The workgroup
-//    barrier sits in the last sub-step, after its fragments are in
-//    registers, so that sub-step's MFMAs cover the first reads of the next
-//    stage; the DMA of step j is spread over the last sub-step of step j-3
-//    and the first three of step j-2.
+//  * Three LDS stages of 48 KB.  A K step (128 bytes) is SUB sub-steps of one
+//    MFMA depth (4 x 32 bytes for int8, 2 x 64 for e4m3); fragments of
+//    sub-step g+1 are read while the MFMAs of g issue, the reads and DMAs
+//    spread between the MFMAs.  A lane's operand bytes are the same K
+//    positions of its row in both operands, so any fixed assignment of K to
+//    operand bytes yields the full dot product.  The workgroup barrier sits
+//    in the last sub-step, after its fragments are in registers, so that
+//    sub-step's MFMAs cover the first reads of the next stage; the DMA of
+//    step j is spread over the last sub-step of step j-3 and the first SUB-1
+//    of step j-2.
 //  * Epilogue: scales and bias are loaded at kernel start; results are
 //    converted with v_cvt_pk_bf16_f32 (round to nearest even), staged in LDS
 //    and written as row-contiguous 16-byte vectors (full 128-byte lines).
 //  * Tiles are ordered so that the workgroups one XCD receives (blockIdx % 8)
 //    form a contiguous range, walked in bands of 8 tile rows, so co-resident
 //    workgroups share A and W panels in that XCD's L2.
+#include <type_traits>
 #include <utility>
 
 #include "launchers.hpp"
@@ -43,7 +51,9 @@ namespace wf {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int BK = 128;  // K bytes per step
 constexpr int BM = 128, BN = 256, WM = 2, WN = 4;
@@ -64,6 +74,29 @@ static_assert(BM * OUT_PITCH <= ST * STAGE, "epilogue tile fits the stages");
 // DATA_FORMAT = 32 bit.  With it, offsets >= num_records read as zero.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 constexpr int kOutOfRange = 0x7ffffff0;
+
+// int8 x int8 -> int32, K = 32 per MFMA (one 16-byte piece per lane).
+struct OpI8 {
+  static constexpr int SUB = 4;
+  static constexpr int PIECES = 1;
+  typedef v16i acc_t;
+  __device__ static acc_t mfma(const v4i* w, const v4i* a, acc_t c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(w[0], a[0], c, 0, 0, 0);
+  }
+};
+// e4m3 x e4m3 -> fp32, K = 64 per MFMA (two 16-byte pieces per lane).  Zero
+// scale operands select the unscaled v_mfma_f32_32x32x64_f8f6f4; format 0
+// is OCP e4m3 for both operands.
+struct OpFp8 {
+  static constexpr int SUB = 2;
+  static constexpr int PIECES = 2;
+  typedef v16f acc_t;
+  __device__ static acc_t mfma(const v4i* w, const v4i* a, acc_t c) {
+    const v8i wv = __builtin_shufflevector(w[0], w[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const v8i av = __builtin_shufflevector(a[0], a[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wv, av, c, 0, 0, 0, 0, 0, 0);
+  }
+};
 
 template <typename F, int... I>
 __device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
@@ -88,13 +121,13 @@ __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds_block, in
 }
 
 struct GemmArgs {
-  const int8_t* a;       // [M, K]
-  const int8_t* w;       // [N, K]
-  const float* sx;       // [M]
-  const float* sw;       // [N]
+  const void* a;         // [M, K] int8 or e4m3
+  const void* w;         // [N, K]
+  const float* sx;       // int8: [M];  e4m3: [1] (s_a)
+  const float* sw;       // int8: [N];  e4m3: [1] (s_w)
   const uint16_t* bias;  // [N] bf16 or null
   uint16_t* y;           // [M, N] bf16 (ldy)
-  int32_t* acc_out;      // [M, N] int32 or null
+  int32_t* acc_out;      // int8 only: [M, N] int32 or null
   int M, N, K;
   int64_t ldy;
   int vec16;             // y and ldy allow 16-byte row stores
@@ -108,8 +141,13 @@ __device__ inline float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + t);
 }
 
-template <bool HAS_BIAS, bool GELU>
-__global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(GemmArgs p) {
+template <typename OP, bool HAS_BIAS, bool GELU>
+__global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
+  constexpr bool kI8 = std::is_same<OP, OpI8>::value;
+  constexpr int SUB = OP::SUB;
+  constexpr int PIECES = OP::PIECES;
+  constexpr int CPS = BK / 16 / SUB;  // 16-byte K chunks per sub-step (2 per lane pair)
+  static_assert(CPS == 2 * PIECES, "sub-step geometry");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[ST * STAGE];
 
   const int tiles_m = (p.M + BM - 1) / BM;
@@ -136,21 +174,26 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(GemmArgs p) {
   float sxv[MI];
   float4 swv[NI][4];
   uint2 bv[NI][4];
+  float scale = 0.f;
+  if constexpr (kI8) {
 #pragma unroll
-  for (int i = 0; i < MI; ++i) sxv[i] = p.sx[min(m0 + wm * (BM / WM) + i * 32 + l32, p.M - 1)];
+    for (int i = 0; i < MI; ++i) sxv[i] = p.sx[min(m0 + wm * (BM / WM) + i * 32 + l32, p.M - 1)];
+  } else {
+    scale = p.sx[0] * p.sw[0];
+  }
 #pragma unroll
   for (int j = 0; j < NI; ++j)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int gn = min(n0 + wn * (BN / WN) + j * 32 + 8 * g + 4 * half, p.N - 4);
-      swv[j][g] = *reinterpret_cast<const float4*>(p.sw + gn);
+      if constexpr (kI8) swv[j][g] = *reinterpret_cast<const float4*>(p.sw + gn);
       bv[j][g] = HAS_BIAS ? *reinterpret_cast<const uint2*>(p.bias + gn) : make_uint2(0, 0);
     }
 
   const __amdgpu_buffer_rsrc_t rsrc_a =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), 0, p.M * p.K, kBufferRsrcWord3);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), 0, p.M * p.K, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsrc_w =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), 0, p.N * p.K, kBufferRsrcWord3);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.w), 0, p.N * p.K, kBufferRsrcWord3);
 
   // DMA block j of this wave: A rows (j * NW + wave) * 8 .. + 7 for j < NBA,
   // else W rows ((j - NBA) * NW + wave) * 8 .. + 7.
@@ -172,48 +215,57 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(GemmArgs p) {
       dma16(rsrc_w, lds + stage * STAGE + A_BYTES + ((j - NBA) * NW + wave) * 1024, off);
   };
 
-  // Fragment reads: row R, K chunk c at R*128 + 16*(c ^ ((R/2)%8)).  The rows
-  // one lane reads differ by multiples of 32, so the swizzle is per lane.
+  // Fragment pieces: sub-step s, lane half h, piece e is K chunk
+  // c = s*CPS + h*PIECES + e of the lane's row R, at R*128 + 16*(c ^ ((R/2)%8)).
+  // The rows one lane reads differ by multiples of 32, so the offsets are per lane.
   const int x = (l32 >> 1) & 7;
-  const int lane_a = (wm * (BM / WM) + l32) * BK + 16 * (half ^ (x & 1));
-  const int lane_b = A_BYTES + (wn * (BN / WN) + l32) * BK + 16 * (half ^ (x & 1));
-  int sub_off[4];
+  const int lane_a = (wm * (BM / WM) + l32) * BK;
+  const int lane_b = A_BYTES + (wn * (BN / WN) + l32) * BK;
+  int koff[SUB][PIECES];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) sub_off[s] = 32 * (s ^ (x >> 1));
+  for (int s = 0; s < SUB; ++s)
+#pragma unroll
+    for (int e = 0; e < PIECES; ++e) koff[s][e] = 16 * ((s * CPS + half * PIECES + e) ^ x);
 
-  v16i acc[NI][MI];
+  typename OP::acc_t acc[NI][MI];
 #pragma unroll
   for (int j = 0; j < NI; ++j)
 #pragma unroll
-    for (int i = 0; i < MI; ++i) acc[j][i] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  v4i fa[2][MI], fw[2][NI];
+    for (int i = 0; i < MI; ++i) acc[j][i] = typename OP::acc_t{};
+  v4i fa[2][MI][PIECES], fw[2][NI][PIECES];
 
-  // Fragment read q (A blocks first, then W blocks) of sub-step s into buffer B.
-  auto frag_read = [&](auto Q, auto B, int stage, int s) {
-    constexpr int q = decltype(Q)::value;
+  // Read o (fragment o / PIECES, A blocks first, piece o % PIECES) of sub-step s into buffer B.
+  auto frag_read = [&](auto O, auto B, int stage, int s) {
+    constexpr int o = decltype(O)::value;
     constexpr int b = decltype(B)::value;
+    constexpr int q = o / PIECES, e = o % PIECES;
     if constexpr (q < MI)
-      fa[b][q] = *reinterpret_cast<const v4i*>(lds + stage * STAGE + lane_a + sub_off[s] + q * 32 * BK);
+      fa[b][q][e] = *reinterpret_cast<const v4i*>(lds + stage * STAGE + lane_a + koff[s][e] + q * 32 * BK);
     else
-      fw[b][q - MI] = *reinterpret_cast<const v4i*>(lds + stage * STAGE + lane_b + sub_off[s] + (q - MI) * 32 * BK);
+      fw[b][q - MI][e] = *reinterpret_cast<const v4i*>(lds + stage * STAGE + lane_b + koff[s][e] + (q - MI) * 32 * BK);
   };
-  // The MFMAs of buffer B, each followed by one of: a read of sub-step rs of
-  // rstage into buffer 1-B, or a DMA of slot SLOT (quarter of a step's DMAs)
-  // for the step at K offset dk0 into dstage.
+  // The MFMAs of buffer B with, spread between them, the reads of sub-step rs
+  // of rstage into buffer 1-B and DMA slot SLOT (of SUB per step) for the
+  // step at K offset dk0 into dstage.
   auto substep = [&](auto B, int rstage, int rs, auto SLOT, int dk0, int dstage) {
     constexpr int b = decltype(B)::value;
     constexpr int slot = decltype(SLOT)::value;
-    constexpr int d_lo = (slot * NDMA + 3) / 4;
-    constexpr int d_hi = ((slot + 1) * NDMA + 3) / 4;
-    constexpr int nd = d_hi - d_lo;
-    constexpr int NMF = MI * NI, NRD = MI + NI;
-    static_assert(nd <= NMF && NRD <= NMF, "interleave");
+    constexpr int d_lo = (slot * NDMA + SUB - 1) / SUB;
+    constexpr int d_hi = ((slot + 1) * NDMA + SUB - 1) / SUB;
+    constexpr int NMF = MI * NI, NRD = (MI + NI) * PIECES;
+    constexpr int NOPS = NRD + d_hi - d_lo;
     static_for<NMF>([&](auto Q) {
       constexpr int q = decltype(Q)::value;
       constexpr int jj = q / MI, ii = q % MI;
-      acc[jj][ii] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[b][jj], fa[b][ii], acc[jj][ii], 0, 0, 0);
-      if constexpr (q < NRD) frag_read(ic<q>{}, ic<b ^ 1>{}, rstage, rs);
-      if constexpr (q >= NMF - nd) dma(ic<d_lo + q - (NMF - nd)>{}, dk0, dstage);
+      acc[jj][ii] = OP::mfma(fw[b][jj], fa[b][ii], acc[jj][ii]);
+      constexpr int o_lo = (q * NOPS + NMF - 1) / NMF, o_hi = ((q + 1) * NOPS + NMF - 1) / NMF;
+      static_for<o_hi - o_lo>([&](auto U) {
+        constexpr int o = o_lo + decltype(U)::value;
+        if constexpr (o < NRD)
+          frag_read(ic<o>{}, ic<b ^ 1>{}, rstage, rs);
+        else
+          dma(ic<d_lo + o - NRD>{}, dk0, dstage);
+      });
       __builtin_amdgcn_sched_barrier(0);
     });
   };
@@ -226,23 +278,24 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(GemmArgs p) {
   wait_counts<NDMA, 0>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  static_for<(NDMA + 3) / 4>([&](auto J) { dma(J, 2 * BK, 2); });
-  static_for<MI + NI>([&](auto Q) { frag_read(Q, ic<0>{}, 0, 0); });
+  static_for<(NDMA + SUB - 1) / SUB>([&](auto J) { dma(J, 2 * BK, 2); });
+  static_for<(MI + NI) * PIECES>([&](auto O) { frag_read(O, ic<0>{}, 0, 0); });
   __builtin_amdgcn_sched_barrier(0);
 
   int c0 = 0, c1 = 1, c2 = 2;  // stages of steps kb, kb+1, kb+2
   for (int kb = 0; kb < nk; ++kb) {
     const int k2 = (kb + 2) * BK;
-    substep(ic<0>{}, c0, 1, ic<1>{}, k2, c2);
-    substep(ic<1>{}, c0, 2, ic<2>{}, k2, c2);
-    substep(ic<0>{}, c0, 3, ic<3>{}, k2, c2);
+    static_for<SUB - 1>([&](auto S) {
+      constexpr int s = decltype(S)::value;
+      substep(ic<s & 1>{}, c0, s + 1, ic<s + 1>{}, k2, c2);
+    });
     // Own reads of this stage done, own DMAs of step kb+1 landed (only step
     // kb+2's may still be in flight); the barrier makes that hold for every wave.
     wait_counts<NDMA, 0>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    substep(ic<1>{}, c1, 0, ic<0>{}, (kb + 3) * BK, c0);
+    substep(ic<(SUB - 1) & 1>{}, c1, 0, ic<0>{}, (kb + 3) * BK, c0);
     const int c = c0;
     c0 = c1;
     c1 = c2;
@@ -263,23 +316,29 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(GemmArgs p) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c = wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
-        float y[4];
-        const float sw4[4] = {swv[j][g].x, swv[j][g].y, swv[j][g].z, swv[j][g].w};
         const uint32_t bb[4] = {bv[j][g].x << 16, bv[j][g].x & 0xffff0000u, bv[j][g].y << 16,
                                 bv[j][g].y & 0xffff0000u};
+        float y[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          y[e] = __fmul_rn(__fmul_rn(static_cast<float>(acc[j][i][4 * g + e]), sxv[i]), sw4[e]);
+          if constexpr (kI8) {
+            const float sw4[4] = {swv[j][g].x, swv[j][g].y, swv[j][g].z, swv[j][g].w};
+            y[e] = __fmul_rn(__fmul_rn(static_cast<float>(acc[j][i][4 * g + e]), sxv[i]), sw4[e]);
+          } else {
+            y[e] = __fmul_rn(acc[j][i][4 * g + e], scale);
+          }
           if (HAS_BIAS) y[e] = __fadd_rn(y[e], __uint_as_float(bb[e]));
           if (GELU) y[e] = gelu_tanh(__uint_as_float(pack_bf16x2_hw(y[e], 0.f) << 16));
         }
         *reinterpret_cast<uint2*>(lds + r * OUT_PITCH + c * 2) =
             make_uint2(pack_bf16x2_hw(y[0], y[1]), pack_bf16x2_hw(y[2], y[3]));
-        if (p.acc_out) {
-          const int gm = m0 + r, gn = n0 + c;
-          if (gm < p.M && gn < p.N)
-            *reinterpret_cast<int4*>(p.acc_out + static_cast<int64_t>(gm) * p.N + gn) =
-                make_int4(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
+        if constexpr (kI8) {
+          if (p.acc_out) {
+            const int gm = m0 + r, gn = n0 + c;
+            if (gm < p.M && gn < p.N)
+              *reinterpret_cast<int4*>(p.acc_out + static_cast<int64_t>(gm) * p.N + gn) =
+                  make_int4(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
+          }
         }
       }
   }
@@ -306,8 +365,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(GemmArgs p) {
   }
 }
 
-GemmArgs make_args(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64_t K, const float* sx,
-                   const float* sw, const void* bias, void* y, int64_t ldy, int32_t* acc_out) {
+GemmArgs make_args(const void* a, const void* w, int64_t M, int64_t N, int64_t K, const float* sx, const float* sw,
+                   const void* bias, void* y, int64_t ldy, int32_t* acc_out) {
   GemmArgs p;
   p.a = a;
   p.w = w;
@@ -324,23 +383,35 @@ GemmArgs make_args(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64
   return p;
 }
 
+template <typename OP>
+int launch(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream, const char* fn) {
+  const int64_t tiles = ((static_cast<int64_t>(p.M) + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD)), block(THREADS);
+  if (bias && gelu)
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, true, true>), grid, block, 0, stream, p);
+  else if (bias)
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, true, false>), grid, block, 0, stream, p);
+  else if (gelu)
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, false, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, false, false>), grid, block, 0, stream, p);
+  return check_launch(fn);
+}
+
 }  // namespace
 
 int launch_gemm_i8(const int8_t* a, const int8_t* w, int64_t M, int64_t N, int64_t K, const float* sx,
                    const float* sw, const void* bias, void* y, int64_t ldy, int32_t* acc_out, int gelu,
                    hipStream_t stream) {
-  const GemmArgs p = make_args(a, w, M, N, K, sx, sw, bias, y, ldy, acc_out);
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD)), block(THREADS);
-  if (bias && gelu)
-    hipLaunchKernelGGL((gemm_i8_kernel<true, true>), grid, block, 0, stream, p);
-  else if (bias)
-    hipLaunchKernelGGL((gemm_i8_kernel<true, false>), grid, block, 0, stream, p);
-  else if (gelu)
-    hipLaunchKernelGGL((gemm_i8_kernel<false, true>), grid, block, 0, stream, p);
-  else
-    hipLaunchKernelGGL((gemm_i8_kernel<false, false>), grid, block, 0, stream, p);
-  return check_launch("wf_gemm_i8");
+  return launch<OpI8>(make_args(a, w, M, N, K, sx, sw, bias, y, ldy, acc_out), bias != nullptr, gelu != 0, stream,
+                      "wf_gemm_i8");
+}
+
+int launch_gemm_fp8_pertensor(const uint8_t* a, const uint8_t* w, int64_t M, int64_t N, int64_t K,
+                              const float* a_scale, const float* w_scale, const void* bias, void* y, int64_t ldy,
+                              hipStream_t stream) {
+  return launch<OpFp8>(make_args(a, w, M, N, K, a_scale, w_scale, bias, y, ldy, nullptr), bias != nullptr, false,
+                       stream, "wf_gemm_fp8_pertensor");
 }
 
 }  // namespace wf
@@ -386,4 +457,46 @@ extern "C" int wf_w8a8_linear(const void* x, int64_t m, int64_t k, int64_t ldx, 
   hipStream_t st = wf::as_stream(stream);
   if (int rc = wf::launch_quant_rows_i8(x, m, k, ldx, ws_q, k, ws_sx, st)) return rc;
   return wf::launch_gemm_i8(ws_q, qw, m, n, k, ws_sx, sw, bias, y, ldy, nullptr, flags & 1, st);
+}
+
+extern "C" int wf_gemm_fp8_pertensor(const uint8_t* a, const uint8_t* w, int64_t m, int64_t n, int64_t k,
+                                     const float* a_scale, const float* w_scale, const void* bias, void* y,
+                                     int64_t ldy, void* stream) {
+  static const char* fn = "wf_gemm_fp8_pertensor";
+  WF_REQUIRE(m >= 0 && n >= 0 && k >= 0 && ldy >= n, WF_E_INVALID, "%s: bad sizes m=%lld n=%lld k=%lld ldy=%lld", fn,
+             (long long)m, (long long)n, (long long)k, (long long)ldy);
+  if (m == 0 || n == 0) return WF_OK;
+  WF_REQUIRE(a && w && a_scale && w_scale && y, WF_E_INVALID, "%s: null pointer", fn);
+  WF_REQUIRE((m + 256) * k < (1ll << 31) - 16 && (n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE,
+             "%s: operands of 2 GiB or more are not supported", fn);
+  WF_REQUIRE(k % 16 == 0 && k > 0, WF_E_SHAPE, "%s: k=%lld must be a positive multiple of 16", fn, (long long)k);
+  WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);
+  WF_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+                 (reinterpret_cast<uintptr_t>(y) & 7u) == 0 && (reinterpret_cast<uintptr_t>(bias) & 7u) == 0,
+             WF_E_ALIGN, "%s: a, w must be 16-byte and y, bias 8-byte aligned", fn);
+  return wf::launch_gemm_fp8_pertensor(a, w, m, n, k, a_scale, w_scale, bias, y, ldy, wf::as_stream(stream));
+}
+
+extern "C" int wf_fp8_linear_pertensor(const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* w_codes,
+                                       const float* w_scale, const void* bias, int64_t n, void* y, int64_t ldy,
+                                       uint8_t* ws_codes, float* ws_scale, float* ws_partials, void* stream) {
+  static const char* fn = "wf_fp8_linear_pertensor";
+  WF_REQUIRE(m >= 0 && n >= 0 && k > 0 && ldx >= k && ldy >= n, WF_E_INVALID,
+             "%s: bad sizes m=%lld n=%lld k=%lld ldx=%lld ldy=%lld", fn, (long long)m, (long long)n, (long long)k,
+             (long long)ldx, (long long)ldy);
+  if (m == 0 || n == 0) return WF_OK;
+  WF_REQUIRE(x && w_codes && w_scale && y && ws_codes && ws_scale && ws_partials, WF_E_INVALID, "%s: null pointer",
+             fn);
+  WF_REQUIRE((m + 256) * k < (1ll << 31) - 16 && (n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE,
+             "%s: operands of 2 GiB or more are not supported", fn);
+  WF_REQUIRE(k % 16 == 0 && ldx % 8 == 0, WF_E_SHAPE, "%s: k %% 16 and ldx %% 8 must be 0", fn);
+  WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);
+  WF_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w_codes) & 15u) == 0 &&
+                 (reinterpret_cast<uintptr_t>(ws_codes) & 15u) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0 &&
+                 (reinterpret_cast<uintptr_t>(bias) & 7u) == 0,
+             WF_E_ALIGN, "%s: x, w_codes, ws_codes must be 16-byte and y, bias 8-byte aligned", fn);
+  hipStream_t st = wf::as_stream(stream);
+  if (int rc = wf::launch_fp8_quant_pertensor(x, m, k, ldx, WF_FP8_TENSOR_ACT, ws_codes, ws_scale, ws_partials, st))
+    return rc;
+  return wf::launch_gemm_fp8_pertensor(ws_codes, w_codes, m, n, k, ws_scale, w_scale, bias, y, ldy, st);
 }

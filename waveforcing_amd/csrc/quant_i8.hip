@@ -113,14 +113,14 @@ int launch_quant_rows_i8(const void* x, int64_t M, int64_t K, int64_t ldx, int8_
   hipLaunchKernelGGL(quant_rows_i8_kernel, dim3(static_cast<uint32_t>((M + kRowsPerBlock - 1) / kRowsPerBlock)),
                      dim3(kThreads), 0, stream,
                      static_cast<const uint16_t*>(x), M, K, ldx, q, ldq, scales);
-  return check_launch("wf_quant_rows_i8");
+  return check_launch("wf_act_quant_i8");
 }
 
 }  // namespace wf
 
-extern "C" int wf_quant_rows_i8(const void* x, int64_t m, int64_t k, int64_t ldx, int8_t* q, float* scales,
+extern "C" int wf_act_quant_i8(const void* x, int64_t m, int64_t k, int64_t ldx, int8_t* q, float* scales,
                                 void* stream) {
-  static const char* fn = "wf_quant_rows_i8";
+  static const char* fn = "wf_act_quant_i8";
   WF_REQUIRE(m >= 0 && k >= 0 && ldx >= k, WF_E_INVALID, "%s: bad sizes m=%lld k=%lld ldx=%lld", fn, (long long)m,
              (long long)k, (long long)ldx);
   if (m == 0 || k == 0) return WF_OK;
