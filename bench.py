@@ -60,10 +60,18 @@ def kv_bytes_per_layer() -> int:
     return 2 * (elems * 2 + elems * 1 + rows * 4)
 
 
-def _timed(fn, steps: int, warmup: int) -> float:
-    """Mean ms per call of ``fn`` over ``steps`` calls, bracketed by HIP events on the current stream."""
-    for _ in range(warmup):
+def _timed(fn, steps: int, warmup: int, min_warm_s: float = 0.0) -> float:
+    """Mean ms per call of ``fn`` over ``steps`` calls, bracketed by HIP events on the current stream.
+
+    Untimed warm-up: ``warmup`` calls, continued until ``min_warm_s`` seconds have passed
+    (clocks of an idle GPU take a while to settle under sustained load)."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < min_warm_s:
         fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -112,7 +120,7 @@ def bench_kv(steps: int, warmup: int, dev: str, which=("pack", "unpack", "pack_l
 
     step_bytes = LAYERS * kv_bytes_per_layer()
     fns = {"pack": pack_all, "unpack": unpack_all, "pack_layers": pack_layers, "unpack_layers": unpack_layers}
-    ms = {name: _timed(fns[name], steps, warmup) for name in which}
+    ms = {name: _timed(fns[name], steps, warmup, min_warm_s=1.0) for name in which}
     out = {"bytes_per_step": step_bytes}
     for name, t in ms.items():
         out[f"ms_{name}"] = t

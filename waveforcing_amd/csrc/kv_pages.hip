@@ -5,9 +5,12 @@
 // is owned by an aligned group of 8 lanes, 16 values (32 B in, 16 B of
 // codes out) per lane, so every code store is one 16-byte vector store and a
 // wave writes 8 rows = 1 KiB of consecutive codes.  The per-row absmax is an
-// 8-lane DPP reduction.  Each workgroup of 256 threads owns 32 * ROWS
-// consecutive rows (ROWS rows per lane group), with all rows' loads issued
-// before any arithmetic.  blockIdx.y selects K (0) or V (1).
+// 8-lane DPP reduction.  Each workgroup of 256 threads owns one block of 32
+// consecutive rows of K or of V.  Blocks are numbered K first, then V, and
+// the workgroups one XCD receives (blockIdx % 8) take a contiguous range of
+// them, so neighbouring rows (which share 64-byte lines of the scale
+// arrays, laid out token-fastest per (page, head)) are written through the
+// same L2.
 //
 // Arithmetic per row, following wave_rt/denoiser/exchange/common.py:145-150
 // with the amax taken per (token, head):
@@ -28,14 +31,26 @@ namespace wf {
 namespace {
 
 constexpr int kHeadDim = 128;
-// Launch shape (rows per 8-lane group, non-temporal hints), chosen by a
-// sweep on MI355X over rows {1, 2, 4, 8} x hints: one row per lane group
-// with streaming (non-temporal) stores is fastest for pack (5.8 TB/s over
-// 30 layers in one launch) and for unpack with streaming loads and stores.
-constexpr int kPackRows = 1;
+// Non-temporal hints, chosen by sweeps on MI355X (rows per lane group
+// {1, 2, 4, 8}, persistent grids, block-to-XCD maps, hints): streaming
+// stores for pack (6.0 TB/s over 30 layers in one launch), streaming loads
+// and stores for unpack (6.0 TB/s).
 constexpr bool kPackNtLoad = false, kPackNtStore = true;
-constexpr int kUnpackRows = 1;
 constexpr bool kUnpackNtLoad = true, kUnpackNtStore = true;
+constexpr int kRowsPerBlock = 32;
+constexpr uint32_t kNumXcd = 8;
+
+// Row block, and whether it is V, of workgroup blockIdx.x over n_items
+// blocks (n_blocks K blocks first, then V blocks when n_items = 2 n_blocks),
+// XCD-contiguous.  Returns false past the end.
+__device__ inline bool block_of(uint32_t n_blocks, uint32_t n_items, uint32_t& blk, bool& is_v) {
+  const uint32_t per_xcd = (n_items + kNumXcd - 1) / kNumXcd;
+  const uint32_t w = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+  if (w >= n_items) return false;
+  is_v = w >= n_blocks;
+  blk = is_v ? w - n_blocks : w;
+  return true;
+}
 
 struct PoolView {
   uint8_t* codes;
@@ -116,47 +131,40 @@ __device__ inline void st16(uint4* p, const uint4& v) {
   }
 }
 
-// ROWS rows per lane group; a workgroup owns 32 * ROWS consecutive rows.
-template <int ROWS, bool NT_LOAD, bool NT_STORE>
+template <bool NT_LOAD, bool NT_STORE>
 __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ k, const uint4* __restrict__ v,
-                                                      int64_t ld_kv, uint32_t n_rows, PageGeom geom, PoolView kpool,
+                                                      int64_t ld_kv, uint32_t n_rows, uint32_t n_blocks,
+                                                      uint32_t n_items, PageGeom geom, PoolView kpool,
                                                       PoolView vpool) {
-  const uint4* __restrict__ src = blockIdx.y == 0 ? k : v;
-  const PoolView pool = blockIdx.y == 0 ? kpool : vpool;
+  uint32_t blk;
+  bool is_v;
+  if (!block_of(n_blocks, n_items, blk, is_v)) return;
+  const uint4* __restrict__ src = is_v ? v : k;
+  const PoolView pool = is_v ? vpool : kpool;
   const uint32_t lane8 = threadIdx.x & 7u;
-  const uint32_t row0 = blockIdx.x * (32u * ROWS) + (threadIdx.x >> 3);
+  const uint32_t r = blk * kRowsPerBlock + (threadIdx.x >> 3);
 
-  uint4 a[ROWS], b[ROWS];
-#pragma unroll
-  for (int u = 0; u < ROWS; ++u) {
-    const uint32_t r = row0 + 32u * u;
-    if (r < n_rows) {
-      uint32_t t, h;
-      geom.heads.divmod(r, t, h);
-      const uint4* p = src + (static_cast<int64_t>(t) * ld_kv + h * kHeadDim) / 8 + lane8 * 2;
-      a[u] = ld16<NT_LOAD>(p);
-      b[u] = ld16<NT_LOAD>(p + 1);
-    } else {
-      a[u] = make_uint4(0, 0, 0, 0);
-      b[u] = a[u];
-    }
+  uint4 a = make_uint4(0, 0, 0, 0), b = a;
+  if (r < n_rows) {
+    uint32_t t, h;
+    geom.heads.divmod(r, t, h);
+    const uint4* p = src + (static_cast<int64_t>(t) * ld_kv + h * kHeadDim) / 8 + lane8 * 2;
+    a = ld16<NT_LOAD>(p);
+    b = ld16<NT_LOAD>(p + 1);
   }
-#pragma unroll
-  for (int u = 0; u < ROWS; ++u) {
-    const uint32_t r = row0 + 32u * u;
-    const float amax = group8_max(absmax8(a[u], b[u]));
-    const float s = scale_from_amax(amax);
-    const float rcp = __frcp_rn(s);
-    uint4 c;
-    c.x = quant4(a[u].x, a[u].y, s, rcp);
-    c.y = quant4(a[u].z, a[u].w, s, rcp);
-    c.z = quant4(b[u].x, b[u].y, s, rcp);
-    c.w = quant4(b[u].z, b[u].w, s, rcp);
-    int64_t code_row, scale_idx;
-    if (r < n_rows && locate(geom, r, code_row, scale_idx)) {
-      st16<NT_STORE>(reinterpret_cast<uint4*>(pool.codes + code_row * kHeadDim) + lane8, c);
-      if (lane8 == 0) pool.scales[scale_idx] = s;
-    }
+  // every lane of the 8-lane group takes part in the reduction
+  const float amax = group8_max(absmax8(a, b));
+  const float s = scale_from_amax(amax);
+  const float rcp = __frcp_rn(s);
+  uint4 c;
+  c.x = quant4(a.x, a.y, s, rcp);
+  c.y = quant4(a.z, a.w, s, rcp);
+  c.z = quant4(b.x, b.y, s, rcp);
+  c.w = quant4(b.z, b.w, s, rcp);
+  int64_t code_row, scale_idx;
+  if (r < n_rows && locate(geom, r, code_row, scale_idx)) {
+    st16<NT_STORE>(reinterpret_cast<uint4*>(pool.codes + code_row * kHeadDim) + lane8, c);
+    if (lane8 == 0) pool.scales[scale_idx] = s;
   }
 }
 
@@ -172,40 +180,28 @@ __device__ inline uint2 dequant4(uint32_t w, float s) {
   return make_uint2(__builtin_bit_cast(uint32_t, blo), __builtin_bit_cast(uint32_t, bhi));
 }
 
-template <int ROWS, bool NT_LOAD, bool NT_STORE>
+template <bool NT_LOAD, bool NT_STORE>
 __global__ __launch_bounds__(256) void kv_unpack_kernel(PoolView kpool, PoolView vpool, uint32_t n_rows,
-                                                        PageGeom geom, uint4* __restrict__ kout,
-                                                        uint4* __restrict__ vout) {
-  const PoolView pool = blockIdx.y == 0 ? kpool : vpool;
-  uint4* __restrict__ dst = blockIdx.y == 0 ? kout : vout;
+                                                        uint32_t n_blocks, uint32_t n_items, PageGeom geom,
+                                                        uint4* __restrict__ kout, uint4* __restrict__ vout) {
+  uint32_t blk;
+  bool is_v;
+  if (!block_of(n_blocks, n_items, blk, is_v)) return;
+  const PoolView pool = is_v ? vpool : kpool;
+  uint4* __restrict__ dst = is_v ? vout : kout;
   const uint32_t lane8 = threadIdx.x & 7u;
-  const uint32_t row0 = blockIdx.x * (32u * ROWS) + (threadIdx.x >> 3);
-
-  uint4 c[ROWS];
-  float s[ROWS];
-  bool ok[ROWS];
-#pragma unroll
-  for (int u = 0; u < ROWS; ++u) {
-    const uint32_t r = row0 + 32u * u;
-    int64_t code_row = 0, scale_idx = 0;
-    ok[u] = r < n_rows && locate(geom, r, code_row, scale_idx);
-    if (ok[u]) {
-      c[u] = ld16<NT_LOAD>(reinterpret_cast<const uint4*>(pool.codes + code_row * kHeadDim) + lane8);
-      s[u] = pool.scales[scale_idx];
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < ROWS; ++u) {
-    if (!ok[u]) continue;
-    const uint32_t r = row0 + 32u * u;
-    const uint2 o0 = dequant4(c[u].x, s[u]);
-    const uint2 o1 = dequant4(c[u].y, s[u]);
-    const uint2 o2 = dequant4(c[u].z, s[u]);
-    const uint2 o3 = dequant4(c[u].w, s[u]);
-    uint4* p = dst + static_cast<int64_t>(r) * (kHeadDim / 8) + lane8 * 2;
-    st16<NT_STORE>(p, make_uint4(o0.x, o0.y, o1.x, o1.y));
-    st16<NT_STORE>(p + 1, make_uint4(o2.x, o2.y, o3.x, o3.y));
-  }
+  const uint32_t r = blk * kRowsPerBlock + (threadIdx.x >> 3);
+  int64_t code_row = 0, scale_idx = 0;
+  if (!(r < n_rows && locate(geom, r, code_row, scale_idx))) return;
+  const uint4 c = ld16<NT_LOAD>(reinterpret_cast<const uint4*>(pool.codes + code_row * kHeadDim) + lane8);
+  const float s = pool.scales[scale_idx];
+  const uint2 o0 = dequant4(c.x, s);
+  const uint2 o1 = dequant4(c.y, s);
+  const uint2 o2 = dequant4(c.z, s);
+  const uint2 o3 = dequant4(c.w, s);
+  uint4* p = dst + static_cast<int64_t>(r) * (kHeadDim / 8) + lane8 * 2;
+  st16<NT_STORE>(p, make_uint4(o0.x, o0.y, o1.x, o1.y));
+  st16<NT_STORE>(p + 1, make_uint4(o2.x, o2.y, o3.x, o3.y));
 }
 
 int check_pool_args(const char* fn, int64_t n_tokens, int32_t n_heads, int32_t head_dim, const int32_t* page_table,
@@ -260,11 +256,12 @@ int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_hea
              WF_E_ALIGN, "%s: K/V and code pools must be 16-byte aligned", fn);
   const uint32_t n_rows = static_cast<uint32_t>(n_tokens * n_heads);
   const wf::PageGeom geom = wf::make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
-  constexpr int kRows = wf::kPackRows;
-  const dim3 grid((n_rows + 32 * kRows - 1) / (32 * kRows), has_v ? 2 : 1);
-  hipLaunchKernelGGL((wf::kv_pack_kernel<kRows, wf::kPackNtLoad, wf::kPackNtStore>), grid, dim3(256), 0, wf::as_stream(stream),
-                     reinterpret_cast<const uint4*>(k), reinterpret_cast<const uint4*>(v), ld_kv, n_rows, geom,
-                     wf::PoolView{k_codes, k_scales}, wf::PoolView{v_codes, v_scales});
+  const uint32_t n_blocks = (n_rows + wf::kRowsPerBlock - 1) / wf::kRowsPerBlock;
+  const uint32_t items = has_v ? 2 * n_blocks : n_blocks;
+  const dim3 grid((items + wf::kNumXcd - 1) / wf::kNumXcd * wf::kNumXcd);
+  hipLaunchKernelGGL((wf::kv_pack_kernel<wf::kPackNtLoad, wf::kPackNtStore>), grid, dim3(256), 0,
+                     wf::as_stream(stream), reinterpret_cast<const uint4*>(k), reinterpret_cast<const uint4*>(v), ld_kv,
+                     n_rows, n_blocks, items, geom, wf::PoolView{k_codes, k_scales}, wf::PoolView{v_codes, v_scales});
   return wf::check_launch(fn);
 }
 
@@ -283,11 +280,12 @@ int wf_fp8_kv_unpack(const uint8_t* k_codes, const uint8_t* v_codes, const float
              WF_E_ALIGN, "%s: outputs and code pools must be 16-byte aligned", fn);
   const uint32_t n_rows = static_cast<uint32_t>(n_tokens * n_heads);
   const wf::PageGeom geom = wf::make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
-  constexpr int kRows = wf::kUnpackRows;
-  const dim3 grid((n_rows + 32 * kRows - 1) / (32 * kRows), has_v ? 2 : 1);
-  hipLaunchKernelGGL((wf::kv_unpack_kernel<kRows, wf::kUnpackNtLoad, wf::kUnpackNtStore>), grid, dim3(256), 0, wf::as_stream(stream),
-                     wf::PoolView{const_cast<uint8_t*>(k_codes), const_cast<float*>(k_scales)},
-                     wf::PoolView{const_cast<uint8_t*>(v_codes), const_cast<float*>(v_scales)}, n_rows, geom,
+  const uint32_t n_blocks = (n_rows + wf::kRowsPerBlock - 1) / wf::kRowsPerBlock;
+  const uint32_t items = has_v ? 2 * n_blocks : n_blocks;
+  const dim3 grid((items + wf::kNumXcd - 1) / wf::kNumXcd * wf::kNumXcd);
+  hipLaunchKernelGGL((wf::kv_unpack_kernel<wf::kUnpackNtLoad, wf::kUnpackNtStore>), grid, dim3(256), 0,
+                     wf::as_stream(stream), wf::PoolView{const_cast<uint8_t*>(k_codes), const_cast<float*>(k_scales)},
+                     wf::PoolView{const_cast<uint8_t*>(v_codes), const_cast<float*>(v_scales)}, n_rows, n_blocks, items, geom,
                      reinterpret_cast<uint4*>(k_out), reinterpret_cast<uint4*>(v_out));
   return wf::check_launch(fn);
 }
