@@ -83,6 +83,9 @@ def _timed(fn, steps: int, warmup: int, min_warm_s: float = 0.0) -> float:
     return start.elapsed_time(stop) / steps
 
 
+WARM_SECONDS = 1.0  # --warm-seconds
+
+
 def bench_kv(steps: int, warmup: int, dev: str, which=("pack", "unpack", "pack_layers", "unpack_layers")):
     """Pack / gather-dequant of 30 layers: one launch over all layers (the
     headline) and one launch per layer (the exchange's per-layer publish)."""
@@ -120,7 +123,7 @@ def bench_kv(steps: int, warmup: int, dev: str, which=("pack", "unpack", "pack_l
 
     step_bytes = LAYERS * kv_bytes_per_layer()
     fns = {"pack": pack_all, "unpack": unpack_all, "pack_layers": pack_layers, "unpack_layers": unpack_layers}
-    ms = {name: _timed(fns[name], steps, warmup, min_warm_s=1.0) for name in which}
+    ms = {name: _timed(fns[name], steps, warmup, min_warm_s=WARM_SECONDS) for name in which}
     out = {"bytes_per_step": step_bytes}
     for name, t in ms.items():
         out[f"ms_{name}"] = t
@@ -290,15 +293,19 @@ def cpu_baseline_kv() -> dict:
 
 
 def main() -> None:
+    global WARM_SECONDS
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
+                    help="minimum untimed warm-up of the KV workloads (profiler runs use 0)")
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention",
                                        "block_1p3b", "block_14b", "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
+    WARM_SECONDS = args.warm_seconds
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path runs on a single GPU); --gpus {args.gpus} is not supported",
               file=sys.stderr)
