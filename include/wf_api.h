@@ -222,16 +222,31 @@ int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads,
 /* y = LayerNorm(x) (fp32 statistics, optional bf16 affine w/b, rounded to
  * bf16), then, if given, the bf16 modulation y = bf16(bf16(y * bf16(1 +
  * scale[f])) + shift[f]) with f = row / frame_tokens (scale/shift bf16
- * [frames][dim]); writes y (bf16, row stride ldo) if out != NULL and its
- * per-token int8 quantization (as wf_act_quant_i8) if q != NULL.
- * dim % 8 == 0, dim <= 5120.  Replaces norm1/norm2 + modulation
- * (naive_rt/rolling_forcing/wan/modules/causal_model.py:381,393-394) and
- * norm3 (:390, model.py:89-99) feeding the W8A8 linears. */
+ * frame rows of stride ld_mod elements); writes y (bf16, row stride ldo) if
+ * out != NULL and its per-token int8 quantization (as wf_act_quant_i8) if
+ * q != NULL.  dim % 8 == 0, dim <= 16384.  Replaces norm1/norm2 +
+ * modulation (naive_rt/rolling_forcing/wan/modules/causal_model.py:381,
+ * 393-394) and norm3 (:390, model.py:89-99) feeding the W8A8 linears. */
 int wf_ln_modulate_quant(const void* x, int64_t T, int32_t dim, int64_t ldx,
                          float eps, const void* w, const void* b,
                          const void* shift, const void* scale,
-                         int32_t frame_tokens, void* out, int64_t ldo,
-                         int8_t* q, float* q_scales, void* stream);
+                         int64_t ld_mod, int32_t frame_tokens, void* out,
+                         int64_t ldo, int8_t* q, float* q_scales,
+                         void* stream);
+
+/* The residual that precedes a norm, fused into it: first, in place,
+ * x = bf16(x + bf16(y * gate[f])) (gate frame rows of stride ld_gate), or
+ * x = bf16(x + y) when gate is NULL, then wf_ln_modulate_quant of the
+ * updated x (out must not alias x).  y == NULL skips the residual.  The
+ * self-attention residual + norm3 (causal_model.py:386-390) and the
+ * cross-attention residual + norm2 + modulation (:390-394). */
+int wf_gate_residual_ln_quant(void* x, int64_t T, int32_t dim, int64_t ldx,
+                              const void* y, int64_t ldy, const void* gate,
+                              int64_t ld_gate, float eps, const void* w,
+                              const void* b, const void* shift,
+                              const void* scale, int64_t ld_mod,
+                              int32_t frame_tokens, void* out, int64_t ldo,
+                              int8_t* q, float* q_scales, void* stream);
 
 /* y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w) over the full row (dim),
  * then, if cos/sin ([T][head_dim/2] fp32) are given, each head's
@@ -244,12 +259,12 @@ int wf_rmsnorm_rope(const void* x, int64_t T, int32_t dim, int64_t ldx,
                     int64_t ldo, void* stream);
 
 /* In place x = bf16(x + bf16(y * gate[row / frame_tokens])), or
- * x = bf16(x + y) when gate is NULL (gate bf16 [frames][dim]).  The gated
- * residuals of causal_model.py:386,397-398 and the cross-attention residual
- * of :390. */
+ * x = bf16(x + y) when gate is NULL (gate bf16 frame rows of stride
+ * ld_gate elements).  The gated residuals of causal_model.py:386,397-398
+ * and the cross-attention residual of :390. */
 int wf_gate_residual(void* x, int64_t ldx, const void* y, int64_t ldy,
-                     const void* gate, int64_t T, int32_t dim,
-                     int32_t frame_tokens, void* stream);
+                     const void* gate, int64_t ld_gate, int64_t T,
+                     int32_t dim, int32_t frame_tokens, void* stream);
 
 #ifdef __cplusplus
 }

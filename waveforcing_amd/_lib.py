@@ -64,13 +64,17 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p,
     ],
     "wf_ln_modulate_quant": [
-        _c_void_p, _i64, _i32, _i64, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32,
+        _c_void_p, _i64, _i32, _i64, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
         _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
+    ],
+    "wf_gate_residual_ln_quant": [
+        _c_void_p, _i64, _i32, _i64, _c_void_p, _i64, _c_void_p, _i64, _f32, _c_void_p, _c_void_p,
+        _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
     ],
     "wf_rmsnorm_rope": [
         _c_void_p, _i64, _i32, _i64, _i32, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
     ],
-    "wf_gate_residual": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i32, _i32, _c_void_p],
+    "wf_gate_residual": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i32, _i32, _c_void_p],
 }
 
 GEMM_GELU_TANH = 1

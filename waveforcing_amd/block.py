@@ -114,11 +114,20 @@ class QLinear:
         return cls(qw, sw, None if b is None else b.to(device).contiguous())
 
 
-def _ln_quant(x, dim, frame_tokens, q, qs, out=None, w=None, b=None, shift=None, scale=None):
+def _ln_quant(x, dim, frame_tokens, q, qs, out=None, w=None, b=None, shift=None, scale=None, res_y=None,
+              res_gate=None):
+    """LayerNorm (+affine, +modulation) and per-token int8 quant of x, optionally after the residual
+    x += res_y (* res_gate) applied in place.  shift/scale/res_gate are frame-row views that share
+    one row stride (columns of the modulation tensor)."""
     T = x.shape[0]
-    _lib.call("wf_ln_modulate_quant", x.data_ptr(), T, dim, x.stride(0), EPS, _lib.ptr(w), _lib.ptr(b),
-              _lib.ptr(shift), _lib.ptr(scale), frame_tokens, _lib.ptr(out), out.stride(0) if out is not None else 0,
-              _lib.ptr(q), _lib.ptr(qs), _lib.stream_handle(x.device))
+    mods = [t for t in (shift, scale, res_gate) if t is not None]
+    ld_mod = mods[0].stride(0) if mods else 0
+    if any(t.stride(0) != ld_mod or t.stride(-1) != 1 for t in mods):
+        raise ValueError("modulation rows must share one row stride with unit column stride")
+    _lib.call("wf_gate_residual_ln_quant", x.data_ptr(), T, dim, x.stride(0), _lib.ptr(res_y),
+              res_y.stride(0) if res_y is not None else 0, _lib.ptr(res_gate), ld_mod, EPS, _lib.ptr(w),
+              _lib.ptr(b), _lib.ptr(shift), _lib.ptr(scale), ld_mod, frame_tokens, _lib.ptr(out),
+              out.stride(0) if out is not None else 0, _lib.ptr(q), _lib.ptr(qs), _lib.stream_handle(x.device))
 
 
 def _rmsnorm_rope(x, head_dim, w, cos, sin, out):
@@ -129,8 +138,8 @@ def _rmsnorm_rope(x, head_dim, w, cos, sin, out):
 
 def _gate_residual(x, y, gate, frame_tokens):
     T, dim = x.shape
-    _lib.call("wf_gate_residual", x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), _lib.ptr(gate), T, dim,
-              frame_tokens, _lib.stream_handle(x.device))
+    _lib.call("wf_gate_residual", x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), _lib.ptr(gate),
+              gate.stride(0) if gate is not None else 0, T, dim, frame_tokens, _lib.stream_handle(x.device))
 
 
 def _linear_i8(x, lin: QLinear, ws_q, ws_s, out, gelu=False):
@@ -218,9 +227,10 @@ class QuantizedWanBlock:
         ft = T // F
         H, hd = self.heads, self.head_dim
         ws = self._workspace(T)
-        # e = (modulation + e).chunk(6)  (causal_model.py:376), bf16
-        es = (self.modulation[0].unsqueeze(0) + e).contiguous()
-        e0, e1, e2, e3, e4, e5 = (es[:, i].contiguous() for i in range(6))
+        # e = (modulation + e).chunk(6)  (causal_model.py:376), bf16: one add; the kernels read
+        # the six [F, dim] chunks as strided frame rows of it.
+        es = self.modulation[0].unsqueeze(0) + e
+        e0, e1, e2, e3, e4, e5 = (es[:, i] for i in range(6))
         aq, as_ = ws["aq"], ws["as_"]
 
         # self-attention: LN1 + modulation + int8 quant -> fused QKV
@@ -235,19 +245,17 @@ class QuantizedWanBlock:
         ctx = PagedKV(pool, context_table, n_context)
         attn_paged_fp8(q.view(T, H, hd), ctx, out=ws["attn"].view(T, H, hd))
         _linear_i8(ws["attn"], self.o, aq, as_, ws["y"])
-        _gate_residual(x, ws["y"], e2, ft)
 
-        # cross-attention: norm3 (affine) + quant -> q, RMSNorm, attention over text, o
-        _ln_quant(x, dim, ft, aq, as_, w=self.norm3_w, b=self.norm3_b)
+        # gated residual + norm3 (affine) + quant -> q, RMSNorm, attention over text, o
+        _ln_quant(x, dim, ft, aq, as_, w=self.norm3_w, b=self.norm3_b, res_y=ws["y"], res_gate=e2)
         gemm_i8(aq, self.cq.w, as_, self.cq.s, self.cq.b, out=ws["y"])
         _rmsnorm_rope(ws["y"], hd, self.cnorm_q, None, None, ws["cq"])
         tk, tv = text_kv
         attn_dense_bf16(ws["cq"].view(T, H, hd), tk, tv, out=ws["attn"].view(T, H, hd))
         _linear_i8(ws["attn"], self.co, aq, as_, ws["y"])
-        _gate_residual(x, ws["y"], None, ft)
 
-        # FFN: LN2 + modulation + quant -> fc_in (+GELU) -> fc_out
-        _ln_quant(x, dim, ft, aq, as_, shift=e3, scale=e4)
+        # residual + LN2 + modulation + quant -> fc_in (+GELU) -> fc_out
+        _ln_quant(x, dim, ft, aq, as_, shift=e3, scale=e4, res_y=ws["y"])
         gemm_i8(aq, self.fc_in.w, as_, self.fc_in.s, self.fc_in.b, gelu=True, out=ws["ffn"])
         _linear_i8(ws["ffn"], self.fc_out, ws["fq"], as_, ws["y"])
         _gate_residual(x, ws["y"], e5, ft)

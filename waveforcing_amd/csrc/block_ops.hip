@@ -4,98 +4,90 @@
 // in bf16, norms compute in fp32 and round to bf16, and every bf16 operation
 // of the modulation and the gated residuals rounds to bf16.
 //
-// One wave per token row (dim up to 5120 = 10 chunks of 8 per lane held in
-// registers), 4 rows per 256-thread workgroup, no LDS: row reductions are
-// wave64 butterflies.
-#include "wf_common.hpp"
+// The norm kernels run on the row engine of rows.hpp: a token row is owned
+// by one wave (dim <= 2048) or one 256-thread workgroup (dim <= 16384), with
+// NC chunks of 8 values per lane fixed at compile time, so a row stays in
+// registers and all of its loads are issued before the first reduction.
+#include "rows.hpp"
 
 namespace wf {
 namespace {
 
-constexpr int kRows = 4;       // rows (waves) per workgroup
-constexpr int kMaxChunks = 10; // 8-element chunks per lane: dim <= 5120
-
-__device__ inline float wave_sum(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-__device__ inline float wave_max(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  return v;
-}
-
-__device__ inline float rbf(float f) { return bf16_bits_to_f32(f32_to_bf16_rne(f)); }
-
-__device__ inline void unpack8(const uint4& w, float* f) {
-  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = bf16_lo_to_f32(u[i]);
-    f[2 * i + 1] = bf16_hi_to_f32(u[i]);
-  }
-}
-__device__ inline uint4 pack8(const float* f) {
-  uint32_t u[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    u[i] = static_cast<uint32_t>(f32_to_bf16_rne(f[2 * i])) |
-           (static_cast<uint32_t>(f32_to_bf16_rne(f[2 * i + 1])) << 16);
-  return make_uint4(u[0], u[1], u[2], u[3]);
-}
-
-// int8 code of x with scale s (reciprocal r): round_half_even(RN(x / s)),
-// as in the per-row quantization kernel.
-__device__ inline int quant_i8(float x, float s, float r) {
-  const float ax = fabsf(x);
-  float q = ax * r;
-  q = fmaf(fmaf(-q, s, ax), r, q);
-  const float k = rintf(q);
-  if (fabsf(fabsf(q - k) - 0.5f) <= q * 1.1920929e-7f) q = __fdiv_rn(ax, s);
-  float qi = fminf(rintf(q), 127.0f);
-  return static_cast<int>(x < 0.f ? -qi : qi);
-}
+using namespace rows;
 
 struct LnArgs {
-  const uint16_t* x;     // bf16 [T, ldx]
+  uint16_t* x;             // bf16 [T, ldx]; updated in place when ry != null
   int64_t ldx;
+  const uint16_t* ry;      // residual addend bf16 [T, ldry] or null
+  int64_t ldry;
+  const uint16_t* rgate;   // residual gate bf16 [frames, ld_rgate] or null
+  int64_t ld_rgate;
   int T, dim;
   float eps;
-  const uint16_t* w;     // LayerNorm affine weight bf16 [dim] or null
-  const uint16_t* b;     // affine bias bf16 [dim] or null
-  const uint16_t* shift; // modulation shift e_a bf16 [F, dim] or null
-  const uint16_t* scale; // modulation scale e_b bf16 [F, dim] (applied as 1 + e_b) or null
-  int frame_tokens;      // tokens per frame (row t uses modulation row t / frame_tokens)
-  uint16_t* out;         // bf16 [T, ldo] or null
+  const uint16_t* w;       // LayerNorm affine weight bf16 [dim] or null
+  const uint16_t* b;       // affine bias bf16 [dim] or null
+  const uint16_t* shift;   // modulation shift e_a bf16 [frames, ld_mod] or null
+  const uint16_t* scale;   // modulation scale e_b bf16 [frames, ld_mod] (as 1 + e_b) or null
+  int64_t ld_mod;
+  int frame_tokens;        // row t uses frame row t / frame_tokens
+  uint16_t* out;           // bf16 [T, ldo] or null
   int64_t ldo;
-  int8_t* q;             // int8 [T, dim] or null
-  float* qs;             // fp32 [T] (with q)
+  int8_t* q;               // int8 [T, dim] or null
+  float* qs;               // fp32 [T] (with q)
 };
 
-// y = LN(x) [* w + b]  (fp32, rounded to bf16: WanLayerNorm, model.py:89-99)
-// y = bf16(bf16(y * bf16(1 + e_b)) + e_a)   (causal_model.py:381,393-394)
+// [x = bf16(x + bf16(ry * rgate[f]))  or  x = bf16(x + ry)]   (causal_model.py:386,390,397-398)
+// y = LN(x) [* w + b]  (fp32 statistics, rounded to bf16: WanLayerNorm, model.py:89-99)
+// y = bf16(bf16(y * bf16(1 + e_b)) + e_a)                     (causal_model.py:381,393-394)
 // optional bf16 output and per-token int8 quantization of y.
+template <int LPR, int NC>
 __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * kRows + (threadIdx.x >> 6);
-  if (t >= a.T) return;
-  const int n_chunks = a.dim / 8;
-  const uint16_t* row = a.x + static_cast<int64_t>(t) * a.ldx;
-  float v[kMaxChunks][8];
+  constexpr int RPB = 256 / LPR;
+  __shared__ float red[3][4];
+  const int lane = static_cast<int>(threadIdx.x) % LPR;
+  const int t = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / LPR;
+  if (t >= a.T) return;  // uniform per row (a wave, or the workgroup for LPR = 256)
+  const int n_chunks = a.dim >> 3;
+  const int f = t / a.frame_tokens;
+  uint16_t* row = a.x + static_cast<int64_t>(t) * a.ldx;
+
+  uint4 xr[NC], yr[NC], gr[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ch = lane + LPR * c;
+    const bool ok = ch < n_chunks;
+    xr[c] = ok ? ld16(row + ch * 8) : make_uint4(0, 0, 0, 0);
+    if (a.ry) yr[c] = ok ? ld16(a.ry + static_cast<int64_t>(t) * a.ldry + ch * 8) : make_uint4(0, 0, 0, 0);
+    if (a.rgate) gr[c] = ok ? ld16(a.rgate + static_cast<int64_t>(f) * a.ld_rgate + ch * 8) : make_uint4(0, 0, 0, 0);
+  }
+  float v[NC][8];
   float sum = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    const int ch = lane + 64 * c;
-    if (ch < n_chunks) {
-      unpack8(*reinterpret_cast<const uint4*>(row + ch * 8), v[c]);
+  for (int c = 0; c < NC; ++c) {
+    unpack8(xr[c], v[c]);
+    if (a.ry) {
+      float y[8];
+      unpack8(yr[c], y);
+      if (a.rgate) {
+        float g[8];
+        unpack8(gr[c], g);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sum += v[c][i];
+        for (int i = 0; i < 8; ++i) y[i] = y[i] * g[i];
+        rbf8(y);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + y[i];
+      rbf8(v[c]);
+      if (lane + LPR * c < n_chunks) st16(row + (lane + LPR * c) * 8, pack8(v[c]));
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum += v[c][i];
   }
-  const float mean = wave_sum(sum) / static_cast<float>(a.dim);
+  const float mean = row_sum<LPR>(sum, red[0]) / static_cast<float>(a.dim);
   float sq = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    if (lane + 64 * c < n_chunks) {
+  for (int c = 0; c < NC; ++c) {
+    if (lane + LPR * c < n_chunks) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float d = v[c][i] - mean;
@@ -103,50 +95,57 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
       }
     }
   }
-  const float var = wave_sum(sq) / static_cast<float>(a.dim);
+  const float var = row_sum<LPR>(sq, red[1]) / static_cast<float>(a.dim);
   const float rstd = 1.0f / sqrtf(var + a.eps);
-  const int f = t / a.frame_tokens;
   float amax = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    const int ch = lane + 64 * c;
+  for (int c = 0; c < NC; ++c) {
+    const int ch = lane + LPR * c;
     if (ch < n_chunks) {
       float wv[8], bv[8], sh[8], sc[8];
-      if (a.w) unpack8(*reinterpret_cast<const uint4*>(a.w + ch * 8), wv);
-      if (a.b) unpack8(*reinterpret_cast<const uint4*>(a.b + ch * 8), bv);
-      if (a.shift) unpack8(*reinterpret_cast<const uint4*>(a.shift + static_cast<int64_t>(f) * a.dim + ch * 8), sh);
-      if (a.scale) unpack8(*reinterpret_cast<const uint4*>(a.scale + static_cast<int64_t>(f) * a.dim + ch * 8), sc);
+      if (a.w) unpack8(ld16(a.w + ch * 8), wv);
+      if (a.b) unpack8(ld16(a.b + ch * 8), bv);
+      if (a.shift) unpack8(ld16(a.shift + static_cast<int64_t>(f) * a.ld_mod + ch * 8), sh);
+      if (a.scale) unpack8(ld16(a.scale + static_cast<int64_t>(f) * a.ld_mod + ch * 8), sc);
+      float y[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float y = (v[c][i] - mean) * rstd;
-        if (a.w) y = y * wv[i];
-        if (a.b) y = y + bv[i];
-        y = rbf(y);
-        if (a.scale) y = rbf(y * rbf(1.0f + sc[i]));
-        if (a.shift) y = rbf(y + sh[i]);
-        v[c][i] = y;
-        amax = fmaxf(amax, fabsf(y));
+        y[i] = (v[c][i] - mean) * rstd;
+        if (a.w) y[i] = y[i] * wv[i];
+        if (a.b) y[i] = y[i] + bv[i];
       }
-      if (a.out) *reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(t) * a.ldo + ch * 8) = pack8(v[c]);
+      rbf8(y);
+      if (a.scale) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sc[i] = 1.0f + sc[i];
+        rbf8(sc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = y[i] * sc[i];
+        rbf8(y);
+      }
+      if (a.shift) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = y[i] + sh[i];
+        rbf8(y);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[c][i] = y[i];
+        amax = fmaxf(amax, fabsf(y[i]));
+      }
+      if (a.out) st16(a.out + static_cast<int64_t>(t) * a.ldo + ch * 8, pack8(v[c]));
     }
   }
   if (a.q) {
-    amax = wave_max(amax);
-    const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-8f);
+    amax = row_max_nonneg<LPR>(amax, red[2]);
+    const float s = i8_scale(amax);
     const float r = __frcp_rn(s);
     if (lane == 0) a.qs[t] = s;
     int8_t* qrow = a.q + static_cast<int64_t>(t) * a.dim;
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) {
-      const int ch = lane + 64 * c;
-      if (ch < n_chunks) {
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) lo |= (static_cast<uint32_t>(quant_i8(v[c][i], s, r)) & 0xffu) << (8 * i);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) hi |= (static_cast<uint32_t>(quant_i8(v[c][4 + i], s, r)) & 0xffu) << (8 * i);
-        *reinterpret_cast<uint2*>(qrow + ch * 8) = make_uint2(lo, hi);
-      }
+    for (int c = 0; c < NC; ++c) {
+      const int ch = lane + LPR * c;
+      if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8_i8(v[c], s, r);
     }
   }
 }
@@ -167,35 +166,41 @@ struct RmsArgs {
 // then, per head, pairs (y[2i], y[2i+1]) rotated by the token's angle i:
 // (a cos - b sin, a sin + b cos) in fp32, rounded to bf16 (is_neox_style=False,
 // backend.py:119-121; causal_rope_apply, causal_model.py:27-55).
+// In place (out == x) is allowed: a row is read whole before it is written.
+template <int LPR, int NC>
 __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RmsArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * kRows + (threadIdx.x >> 6);
+  constexpr int RPB = 256 / LPR;
+  __shared__ float red[4];
+  const int lane = static_cast<int>(threadIdx.x) % LPR;
+  const int t = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / LPR;
   if (t >= a.T) return;
-  const int n_chunks = a.dim / 8;
+  const int n_chunks = a.dim >> 3;
   const uint16_t* row = a.x + static_cast<int64_t>(t) * a.ldx;
-  float v[kMaxChunks][8];
+  float v[NC][8];
   float sq = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    const int ch = lane + 64 * c;
-    if (ch < n_chunks) {
-      unpack8(*reinterpret_cast<const uint4*>(row + ch * 8), v[c]);
+  for (int c = 0; c < NC; ++c) {
+    const int ch = lane + LPR * c;
+    unpack8(ch < n_chunks ? ld16(row + ch * 8) : make_uint4(0, 0, 0, 0), v[c]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sq += v[c][i] * v[c][i];
-    }
+    for (int i = 0; i < 8; ++i) sq += v[c][i] * v[c][i];
   }
-  const float ms = wave_sum(sq) / static_cast<float>(a.dim);
+  const float ms = row_sum<LPR>(sq, red) / static_cast<float>(a.dim);
   const float rn = 1.0f / sqrtf(ms + a.eps);
   const int half = a.head_dim / 2;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    const int ch = lane + 64 * c;
+  for (int c = 0; c < NC; ++c) {
+    const int ch = lane + LPR * c;
     if (ch < n_chunks) {
       float wv[8];
-      unpack8(*reinterpret_cast<const uint4*>(a.w + ch * 8), wv);
+      unpack8(ld16(a.w + ch * 8), wv);
       float y[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = rbf(rbf(v[c][i] * rn) * wv[i]);
+      for (int i = 0; i < 8; ++i) y[i] = v[c][i] * rn;
+      rbf8(y);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = y[i] * wv[i];
+      rbf8(y);
       if (a.cos) {
         // element e = ch * 8 + i; pair index within the head: (e % head_dim) / 2
         const int p0 = ((ch * 8) % a.head_dim) / 2;
@@ -210,7 +215,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RmsArgs a) {
           y[2 * j + 1] = x0 * sn[j] + x1 * cs[j];
         }
       }
-      *reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(t) * a.ldo + ch * 8) = pack8(y);
+      st16(a.out + static_cast<int64_t>(t) * a.ldo + ch * 8, pack8(y));
     }
   }
 }
@@ -219,88 +224,129 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RmsArgs a) {
 // or x = bf16(x + y) without a gate (cross-attention residual, :390).
 __global__ __launch_bounds__(256) void gate_residual_kernel(uint16_t* __restrict__ x, int64_t ldx,
                                                             const uint16_t* __restrict__ y, int64_t ldy,
-                                                            const uint16_t* __restrict__ gate, int T, int dim,
-                                                            int frame_tokens) {
+                                                            const uint16_t* __restrict__ gate, int64_t ld_gate,
+                                                            int T, int dim, int frame_tokens) {
   const int n_chunks = dim / 8;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= static_cast<int64_t>(T) * n_chunks) return;
   const int t = static_cast<int>(idx / n_chunks);
   const int ch = static_cast<int>(idx % n_chunks);
   float xv[8], yv[8], g[8];
-  uint4* xp = reinterpret_cast<uint4*>(x + static_cast<int64_t>(t) * ldx + ch * 8);
-  unpack8(*xp, xv);
-  unpack8(*reinterpret_cast<const uint4*>(y + static_cast<int64_t>(t) * ldy + ch * 8), yv);
+  uint16_t* xp = x + static_cast<int64_t>(t) * ldx + ch * 8;
+  unpack8(ld16(xp), xv);
+  unpack8(ld16(y + static_cast<int64_t>(t) * ldy + ch * 8), yv);
   if (gate) {
-    unpack8(*reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(t / frame_tokens) * dim + ch * 8), g);
+    unpack8(ld16(gate + static_cast<int64_t>(t / frame_tokens) * ld_gate + ch * 8), g);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = rbf(xv[i] + rbf(yv[i] * g[i]));
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = rbf(xv[i] + yv[i]);
+    for (int i = 0; i < 8; ++i) yv[i] = yv[i] * g[i];
+    rbf8(yv);
   }
-  *xp = pack8(xv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xv[i] = xv[i] + yv[i];
+  rbf8(xv);
+  st16(xp, pack8(xv));
 }
 
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int launch_ln(const LnArgs& a, hipStream_t stream, const char* fn) {
+  int lpr = 0, nc = 0;
+  pick_shape(a.dim / 8, lpr, nc);
+  const uint32_t grid = static_cast<uint32_t>((a.T + 256 / lpr - 1) / (256 / lpr));
+  dispatch_shape(lpr, nc, [&](auto L, auto C) {
+    hipLaunchKernelGGL((ln_mod_quant_kernel<decltype(L)::value, decltype(C)::value>), dim3(grid), dim3(256), 0,
+                       stream, a);
+  });
+  return check_launch(fn);
+}
 
 }  // namespace
 }  // namespace wf
 
 extern "C" {
 
-int wf_ln_modulate_quant(const void* x, int64_t T, int32_t dim, int64_t ldx, float eps, const void* w, const void* b,
-                         const void* shift, const void* scale, int32_t frame_tokens, void* out, int64_t ldo,
-                         int8_t* q, float* q_scales, void* stream) {
-  static const char* fn = "wf_ln_modulate_quant";
+int wf_gate_residual_ln_quant(void* x, int64_t T, int32_t dim, int64_t ldx, const void* y, int64_t ldy,
+                              const void* gate, int64_t ld_gate, float eps, const void* w, const void* b,
+                              const void* shift, const void* scale, int64_t ld_mod, int32_t frame_tokens, void* out,
+                              int64_t ldo, int8_t* q, float* q_scales, void* stream) {
+  static const char* fn = "wf_gate_residual_ln_quant";
   WF_REQUIRE(T >= 0 && dim > 0 && ldx >= dim && frame_tokens > 0, WF_E_INVALID, "%s: bad sizes", fn);
-  WF_REQUIRE(dim % 8 == 0 && dim <= 64 * 8 * wf::kMaxChunks, WF_E_SHAPE, "%s: dim=%d (need %% 8 == 0, <= 5120)", fn,
-             dim);
+  WF_REQUIRE(dim % 8 == 0 && dim <= 16384, WF_E_SHAPE, "%s: dim=%d (need %% 8 == 0, <= 16384)", fn, dim);
   if (T == 0) return WF_OK;
   WF_REQUIRE(x && (out || q), WF_E_INVALID, "%s: null input or no output", fn);
+  WF_REQUIRE(!y || ldy >= dim, WF_E_INVALID, "%s: ldy < dim", fn);
+  WF_REQUIRE(!gate || y, WF_E_INVALID, "%s: gate without y", fn);
+  WF_REQUIRE(!gate || ld_gate >= dim, WF_E_INVALID, "%s: ld_gate < dim", fn);
+  WF_REQUIRE(!(shift || scale) || ld_mod >= dim, WF_E_INVALID, "%s: ld_mod < dim", fn);
   WF_REQUIRE(!q || q_scales, WF_E_INVALID, "%s: q without q_scales", fn);
   WF_REQUIRE(!out || ldo >= dim, WF_E_INVALID, "%s: ldo < dim", fn);
-  WF_REQUIRE(wf::a16(x) && ldx % 8 == 0 && (!out || (wf::a16(out) && ldo % 8 == 0)) && (!q || (reinterpret_cast<uintptr_t>(q) & 7u) == 0) &&
-                 (!w || wf::a16(w)) && (!b || wf::a16(b)) && (!shift || wf::a16(shift)) && (!scale || wf::a16(scale)),
+  WF_REQUIRE(!out || !y || out != x, WF_E_INVALID, "%s: out must not alias x when a residual is applied", fn);
+  WF_REQUIRE(wf::a16(x) && ldx % 8 == 0 && (!out || (wf::a16(out) && ldo % 8 == 0)) &&
+                 (!y || (wf::a16(y) && ldy % 8 == 0)) && (!gate || (wf::a16(gate) && ld_gate % 8 == 0)) &&
+                 (!q || (reinterpret_cast<uintptr_t>(q) & 7u) == 0) && (!w || wf::a16(w)) && (!b || wf::a16(b)) &&
+                 (!shift || wf::a16(shift)) && (!scale || wf::a16(scale)) && ((!shift && !scale) || ld_mod % 8 == 0),
              WF_E_ALIGN, "%s: tensors must be 16-byte aligned with row strides %% 8 == 0", fn);
-  wf::LnArgs a{static_cast<const uint16_t*>(x), ldx, static_cast<int>(T), dim, eps,
+  wf::LnArgs a{static_cast<uint16_t*>(x), ldx, static_cast<const uint16_t*>(y), ldy,
+               static_cast<const uint16_t*>(gate), ld_gate, static_cast<int>(T), dim, eps,
                static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),
-               static_cast<const uint16_t*>(shift), static_cast<const uint16_t*>(scale), frame_tokens,
+               static_cast<const uint16_t*>(shift), static_cast<const uint16_t*>(scale), ld_mod, frame_tokens,
                static_cast<uint16_t*>(out), ldo, q, q_scales};
-  hipLaunchKernelGGL(wf::ln_mod_quant_kernel, dim3(static_cast<uint32_t>((T + wf::kRows - 1) / wf::kRows)),
-                     dim3(256), 0, wf::as_stream(stream), a);
-  return wf::check_launch(fn);
+  return wf::launch_ln(a, wf::as_stream(stream), fn);
+}
+
+int wf_ln_modulate_quant(const void* x, int64_t T, int32_t dim, int64_t ldx, float eps, const void* w, const void* b,
+                         const void* shift, const void* scale, int64_t ld_mod, int32_t frame_tokens, void* out,
+                         int64_t ldo, int8_t* q, float* q_scales, void* stream) {
+  return wf_gate_residual_ln_quant(const_cast<void*>(x), T, dim, ldx, nullptr, 0, nullptr, 0, eps, w, b, shift, scale,
+                                   ld_mod, frame_tokens, out, ldo, q, q_scales, stream);
 }
 
 int wf_rmsnorm_rope(const void* x, int64_t T, int32_t dim, int64_t ldx, int32_t head_dim, float eps, const void* w,
                     const float* cos, const float* sin, void* out, int64_t ldo, void* stream) {
   static const char* fn = "wf_rmsnorm_rope";
   WF_REQUIRE(T >= 0 && dim > 0 && head_dim > 0 && ldx >= dim && ldo >= dim, WF_E_INVALID, "%s: bad sizes", fn);
-  WF_REQUIRE(dim % 8 == 0 && dim <= 64 * 8 * wf::kMaxChunks && dim % head_dim == 0 && head_dim % 8 == 0, WF_E_SHAPE,
+  WF_REQUIRE(dim % 8 == 0 && dim <= 16384 && dim % head_dim == 0 && head_dim % 8 == 0, WF_E_SHAPE,
              "%s: dim=%d head_dim=%d unsupported", fn, dim, head_dim);
   if (T == 0) return WF_OK;
   WF_REQUIRE(x && w && out && ((cos == nullptr) == (sin == nullptr)), WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE(wf::a16(x) && wf::a16(w) && wf::a16(out) && ldx % 8 == 0 && ldo % 8 == 0 && (!cos || (wf::a16(cos) && wf::a16(sin))),
+  WF_REQUIRE(wf::a16(x) && wf::a16(w) && wf::a16(out) && ldx % 8 == 0 && ldo % 8 == 0 &&
+                 (!cos || (wf::a16(cos) && wf::a16(sin))),
              WF_E_ALIGN, "%s: tensors must be 16-byte aligned with row strides %% 8 == 0", fn);
+  {
+    // In place needs the same rows; otherwise the output must not overlap the input rows.
+    const char* xb = static_cast<const char*>(x);
+    const char* ob = static_cast<const char*>(out);
+    const int64_t span_x = ((T - 1) * ldx + dim) * 2, span_o = ((T - 1) * ldo + dim) * 2;
+    WF_REQUIRE((out == x && ldo == ldx) || ob + span_o <= xb || xb + span_x <= ob, WF_E_INVALID,
+               "%s: out overlaps x without being x itself", fn);
+  }
   wf::RmsArgs a{static_cast<const uint16_t*>(x), ldx, static_cast<int>(T), dim, head_dim, eps,
                 static_cast<const uint16_t*>(w), cos, sin, static_cast<uint16_t*>(out), ldo};
-  hipLaunchKernelGGL(wf::rmsnorm_rope_kernel, dim3(static_cast<uint32_t>((T + wf::kRows - 1) / wf::kRows)),
-                     dim3(256), 0, wf::as_stream(stream), a);
+  int lpr = 0, nc = 0;
+  wf::rows::pick_shape(dim / 8, lpr, nc);
+  const uint32_t grid = static_cast<uint32_t>((T + 256 / lpr - 1) / (256 / lpr));
+  wf::rows::dispatch_shape(lpr, nc, [&](auto L, auto C) {
+    hipLaunchKernelGGL((wf::rmsnorm_rope_kernel<decltype(L)::value, decltype(C)::value>), dim3(grid), dim3(256), 0,
+                       wf::as_stream(stream), a);
+  });
   return wf::check_launch(fn);
 }
 
-int wf_gate_residual(void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate, int64_t T, int32_t dim,
-                     int32_t frame_tokens, void* stream) {
+int wf_gate_residual(void* x, int64_t ldx, const void* y, int64_t ldy, const void* gate, int64_t ld_gate, int64_t T,
+                     int32_t dim, int32_t frame_tokens, void* stream) {
   static const char* fn = "wf_gate_residual";
   WF_REQUIRE(T >= 0 && dim > 0 && ldx >= dim && ldy >= dim && frame_tokens > 0, WF_E_INVALID, "%s: bad sizes", fn);
+  WF_REQUIRE(!gate || ld_gate >= dim, WF_E_INVALID, "%s: ld_gate < dim", fn);
   WF_REQUIRE(dim % 8 == 0, WF_E_SHAPE, "%s: dim %% 8 != 0", fn);
   if (T == 0) return WF_OK;
   WF_REQUIRE(x && y, WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE(wf::a16(x) && wf::a16(y) && (!gate || wf::a16(gate)) && ldx % 8 == 0 && ldy % 8 == 0, WF_E_ALIGN,
-             "%s: tensors must be 16-byte aligned with row strides %% 8 == 0", fn);
+  WF_REQUIRE(wf::a16(x) && wf::a16(y) && (!gate || (wf::a16(gate) && ld_gate % 8 == 0)) && ldx % 8 == 0 &&
+                 ldy % 8 == 0,
+             WF_E_ALIGN, "%s: tensors must be 16-byte aligned with row strides %% 8 == 0", fn);
   const int64_t n = T * (dim / 8);
   hipLaunchKernelGGL(wf::gate_residual_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0,
                      wf::as_stream(stream), static_cast<uint16_t*>(x), ldx, static_cast<const uint16_t*>(y), ldy,
-                     static_cast<const uint16_t*>(gate), static_cast<int>(T), dim, frame_tokens);
+                     static_cast<const uint16_t*>(gate), ld_gate, static_cast<int>(T), dim, frame_tokens);
   return wf::check_launch(fn);
 }
 

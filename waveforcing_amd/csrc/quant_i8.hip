@@ -14,12 +14,12 @@
 // those elements are recomputed with a full IEEE division, so the result is
 // round_half_even(RN(x / s)) exactly.
 //
-// One wave per row, 4 rows per 256-thread workgroup: each lane owns chunks
-// of 8 consecutive bf16 (one 16-byte load, one 8-byte store of codes); rows
-// up to 4096 wide stay in registers between the absmax reduction (a wave64
-// butterfly, no LDS) and the quantization pass, longer rows are read twice
-// (the second read is served by L2).
+// Rows up to 16384 wide run on the row engine of rows.hpp (one wave per row
+// up to 2048, one workgroup per row above; the row stays in registers
+// between the absmax reduction and the quantization pass).  Wider rows use
+// one wave per row that reads the row twice (the second read is served by L2).
 #include "launchers.hpp"
+#include "rows.hpp"
 #include "wf_common.hpp"
 
 namespace wf {
@@ -106,13 +106,55 @@ __global__ __launch_bounds__(kThreads) void quant_rows_i8_kernel(const uint16_t*
     *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(*reinterpret_cast<const uint4*>(row + ch * 8), s, r);
 }
 
+// Row-engine variant: LPR lanes per row, NC chunks of 8 per lane.
+template <int LPR, int NC>
+__global__ __launch_bounds__(256) void quant_rows_i8_row_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                                int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
+                                                                float* __restrict__ scales) {
+  constexpr int RPB = 256 / LPR;
+  __shared__ float red[4];
+  const int lane = static_cast<int>(threadIdx.x) % LPR;
+  const int m = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / LPR;
+  if (m >= M) return;  // uniform per row
+  const int n_chunks = K >> 3;
+  const uint16_t* row = x + static_cast<int64_t>(m) * ldx;
+  uint4 reg[NC];
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ch = lane + LPR * c;
+    reg[c] = ch < n_chunks ? rows::ld16(row + ch * 8) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c) amax = fmaxf(amax, amax8(reg[c]));
+  amax = rows::row_max_nonneg<LPR>(amax, red);
+  const float s = rows::i8_scale(amax);
+  const float r = __frcp_rn(s);
+  if (lane == 0) scales[m] = s;
+  int8_t* qrow = q + static_cast<int64_t>(m) * ldq;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ch = lane + LPR * c;
+    if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(reg[c], s, r);
+  }
+}
+
 }  // namespace
 
 int launch_quant_rows_i8(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* scales,
                          hipStream_t stream) {
-  hipLaunchKernelGGL(quant_rows_i8_kernel, dim3(static_cast<uint32_t>((M + kRowsPerBlock - 1) / kRowsPerBlock)),
-                     dim3(kThreads), 0, stream,
-                     static_cast<const uint16_t*>(x), M, K, ldx, q, ldq, scales);
+  int lpr = 0, nc = 0;
+  if (rows::pick_shape(K / 8, lpr, nc)) {
+    const uint32_t grid = static_cast<uint32_t>((M + 256 / lpr - 1) / (256 / lpr));
+    rows::dispatch_shape(lpr, nc, [&](auto L, auto C) {
+      hipLaunchKernelGGL((quant_rows_i8_row_kernel<decltype(L)::value, decltype(C)::value>), dim3(grid), dim3(256),
+                         0, stream, static_cast<const uint16_t*>(x), static_cast<int>(M), static_cast<int>(K), ldx, q,
+                         ldq, scales);
+    });
+  } else {
+    hipLaunchKernelGGL(quant_rows_i8_kernel, dim3(static_cast<uint32_t>((M + kRowsPerBlock - 1) / kRowsPerBlock)),
+                       dim3(kThreads), 0, stream, static_cast<const uint16_t*>(x), M, K, ldx, q, ldq, scales);
+  }
   return check_launch("wf_act_quant_i8");
 }
 
