@@ -18,23 +18,38 @@
 // on invalid pages read as zero through the buffer descriptors), then
 // bf16(code * s) into LDS as [key][d] rows.  The loads of tile i+2 fly while
 // tile i computes, and tile i+1 is dequantized into the other LDS stage
-// between the score and the PV matrix products of tile i.
+// while the score matrix products of tile i run.
 //
 // The score block is computed transposed, S^T = K Q^T with
 // v_mfma_f32_32x32x16_bf16 (K fragment first operand, Q^T fragment second,
 // Q^T kept in registers for the whole kernel): each lane then holds one
 // query column and 16 keys per 32-key block, so the row max is an in-lane
-// max plus one exchange with lane ^ 32, and the lane's P values are directly
-// the second operand of O^T = V^T P^T.  The V^T operand is read from the
-// [key][d] rows with ds_read_b64_tr_b16 (a 16-lane transposing read), the
-// source rows chosen so the key order of each lane's operand matches its P
-// registers.
+// max plus one v_permlane32_swap with lane ^ 32, and the lane's P values
+// are directly the second operand of O^T = V^T P^T.  The V^T operand is
+// read from the [key][d] rows with ds_read_b64_tr_b16 (a 16-lane transposing
+// read), the source rows chosen so the key order of each lane's operand
+// matches its P registers.
+//
+// Schedule of one tile (straight-line apart from the rare rescale; the last
+// tile is peeled for the masking of keys past n_kv, tiles past the end load
+// as zeros into the stage nobody reads any more):
+//   * the 16 K fragments are read first, then the 16 score MFMAs alternate
+//     with the next tile's dequantization (sched_group_barrier: 1 MFMA, 5
+//     VALU), whose result is then written to the other stage;
+//   * the 32 V^T reads are issued before the softmax, so they land during it;
+//   * each 16-key step's exponentials feed its 4 PV MFMAs, so the
+//     exponentials of step t+1 issue under the MFMAs of step t.
+// A wave issues a VALU instruction at most every ~8 cycles on gfx950, so
+// the vector work only hides when it sits between the wave's own MFMAs.
 //
 // Softmax in base 2 with the scale folded into one FMA per score, and lazy
 // rescaling: the running maximum used in the exponent is raised only when a
 // tile's maximum exceeds it by more than kTau (log2 units), so P <= 2^kTau
 // and the O / row-sum rescale is rare; the final normalisation divides by
 // the row sum taken against the same maximum, so the result is unchanged.
+// K stays exactly bf16(code * s): with heavy-tailed K the scores reach
+// magnitudes where any further rounding of K (e.g. folding the scale into
+// it) moves P by percents.
 #include <utility>
 
 #include "fastdiv.hpp"
@@ -113,6 +128,26 @@ __device__ inline v4s read_tr(const uint8_t* addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(addr));
 }
 
+// max / sum of v over lanes l and l ^ 32 (v_permlane32_swap): a lane's two
+// halves of a score column.  The swap is inline asm: the ROCm 7.2 compiler
+// reads both results of __builtin_amdgcn_permlane32_swap from the
+// destination register (r0 + r1 becomes 2 r0).  The s_nop is the VALU ->
+// permlane wait state the compiler emits before the builtin; the asm is not
+// volatile, so it schedules like any other instruction.
+__device__ inline void swap_halves(float& lo, float& hi) {
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+}
+__device__ inline float pair_max(float v) {
+  float a = v, b = v;
+  swap_halves(a, b);
+  return fmaxf(a, b);
+}
+__device__ inline float pair_sum(float v) {
+  float a = v, b = v;
+  swap_halves(a, b);
+  return a + b;
+}
+
 template <bool DENSE>
 __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
@@ -165,56 +200,73 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // most two pages (page_tokens >= 64, checked on the host); the page
   // lookups are uniform across the workgroup.
   auto load_tile = [&](int t0) {
-    const int key = t0 + skey;
     if constexpr (DENSE) {
-      const int off = key < p.n_kv ? (key * static_cast<int>(p.ldkv) + h * D + schunk * 16) * 2 : kOutOfRange;
-      const int off1 = off == kOutOfRange ? off : off + 16;
-      sk0 = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
-      sk1 = __builtin_amdgcn_raw_buffer_load_b128(rk, off1, 0, 0);
-      sv0 = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
-      sv1 = __builtin_amdgcn_raw_buffer_load_b128(rv, off1, 0, 0);
+      const int key = min(t0 + skey, p.n_kv);
+      const uint32_t off = static_cast<uint32_t>((key * static_cast<int>(p.ldkv) + h * D + schunk * 16) * 2) +
+                           (key < p.n_kv ? 0u : static_cast<uint32_t>(kOutOfRange));
+      sk0 = __builtin_amdgcn_raw_buffer_load_b128(rk, static_cast<int>(off), 0, 0);
+      sk1 = __builtin_amdgcn_raw_buffer_load_b128(rk, static_cast<int>(off + 16), 0, 0);
+      sv0 = __builtin_amdgcn_raw_buffer_load_b128(rv, static_cast<int>(off), 0, 0);
+      sv1 = __builtin_amdgcn_raw_buffer_load_b128(rv, static_cast<int>(off + 16), 0, 0);
     } else {
+      // Branch-free: past n_kv or on an invalid page the offsets are pushed
+      // beyond the buffer ranges (>= kOutOfRange > pool size), which read as zero.
       uint32_t lp, rip;
       p.page_div.divmod(static_cast<uint32_t>(t0), lp, rip);
-      const int pg0 = static_cast<int>(lp) < p.n_table ? p.table[lp] : -1;
-      const int pg1 = static_cast<int>(lp) + 1 < p.n_table ? p.table[lp + 1] : -1;
-      const bool ok0 = pg0 >= 0 && pg0 < p.pool_pages;
-      const bool ok1 = pg1 >= 0 && pg1 < p.pool_pages;
-      const int split = p.page_tokens - static_cast<int>(rip);
-      const int cb0 = ((pg0 * p.page_tokens + static_cast<int>(rip)) * p.H + h) * D;
-      const int cb1 = (pg1 * p.page_tokens * p.H + h) * D - split * HD;
-      const int sb0 = ((pg0 * p.H + h) * p.page_tokens + static_cast<int>(rip)) * 4;
-      const int sb1 = (pg1 * p.H + h) * p.page_tokens * 4 - split * 4;
+      const int lpi = static_cast<int>(lp), r0 = static_cast<int>(rip);
+      const int last = p.n_table - 1;  // >= 0 whenever n_kv > 0
+      int pg0 = p.table[min(lpi, last)];
+      int pg1 = p.table[min(lpi + 1, last)];
+      const bool ok0 = lpi <= last && pg0 >= 0 && pg0 < p.pool_pages;
+      const bool ok1 = lpi + 1 <= last && pg1 >= 0 && pg1 < p.pool_pages;
+      pg0 = ok0 ? pg0 : 0;
+      pg1 = ok1 ? pg1 : 0;
+      const int split = p.page_tokens - r0;
       const bool first = skey < split;
-      const bool ok = key < p.n_kv && (first ? ok0 : ok1);
-      const int co = ok ? (first ? cb0 : cb1) + skey * HD + schunk * 16 : kOutOfRange;
-      const int so = ok ? (first ? sb0 : sb1) + skey * 4 : kOutOfRange;
-      sk0 = __builtin_amdgcn_raw_buffer_load_b128(rk, co, 0, 0);
-      sv0 = __builtin_amdgcn_raw_buffer_load_b128(rv, co, 0, 0);
-      ssk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsk, so, 0, 0));
-      ssv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsv, so, 0, 0));
+      const int pg = first ? pg0 : pg1;
+      const int row = first ? r0 + skey : skey - split;
+      const bool ok = (t0 + skey < p.n_kv) && (first ? ok0 : ok1);
+      const uint32_t far = ok ? 0u : static_cast<uint32_t>(kOutOfRange);
+      const uint32_t co = static_cast<uint32_t>(((pg * p.page_tokens + row) * p.H + h) * D + schunk * 16) + far;
+      const uint32_t so = static_cast<uint32_t>(((pg * p.H + h) * p.page_tokens + row) * 4) + far;
+      sk0 = __builtin_amdgcn_raw_buffer_load_b128(rk, static_cast<int>(co), 0, 0);
+      sv0 = __builtin_amdgcn_raw_buffer_load_b128(rv, static_cast<int>(co), 0, 0);
+      ssk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsk, static_cast<int>(so), 0, 0));
+      ssv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsv, static_cast<int>(so), 0, 0));
     }
   };
 
-  // Write the staged tile into LDS stage `buf` as bf16 [key][d] rows.
-  auto store_tile = [&](int buf) {
-    uint4* dk = reinterpret_cast<uint4*>(lds + buf * STAGE + skey * KP + schunk * 32);
-    uint4* dv = reinterpret_cast<uint4*>(lds + buf * STAGE + K_TILE + skey * VP + schunk * 32);
+  // The staged tile as bf16 [key][d] row pieces (registers only), and their
+  // write into LDS stage `buf`.
+  auto dequant_tile = [&](uint4* out) {
     if constexpr (DENSE) {
-      dk[0] = make_uint4(sk0[0], sk0[1], sk0[2], sk0[3]);
-      dk[1] = make_uint4(sk1[0], sk1[1], sk1[2], sk1[3]);
-      dv[0] = make_uint4(sv0[0], sv0[1], sv0[2], sv0[3]);
-      dv[1] = make_uint4(sv1[0], sv1[1], sv1[2], sv1[3]);
+      out[0] = make_uint4(sk0[0], sk0[1], sk0[2], sk0[3]);
+      out[1] = make_uint4(sk1[0], sk1[1], sk1[2], sk1[3]);
+      out[2] = make_uint4(sv0[0], sv0[1], sv0[2], sv0[3]);
+      out[3] = make_uint4(sv1[0], sv1[1], sv1[2], sv1[3]);
     } else {
       const uint2 a = dequant4_bf16(sk0[0], ssk), b = dequant4_bf16(sk0[1], ssk);
       const uint2 c = dequant4_bf16(sk0[2], ssk), d = dequant4_bf16(sk0[3], ssk);
-      dk[0] = make_uint4(a.x, a.y, b.x, b.y);
-      dk[1] = make_uint4(c.x, c.y, d.x, d.y);
+      out[0] = make_uint4(a.x, a.y, b.x, b.y);
+      out[1] = make_uint4(c.x, c.y, d.x, d.y);
       const uint2 e = dequant4_bf16(sv0[0], ssv), f = dequant4_bf16(sv0[1], ssv);
       const uint2 g = dequant4_bf16(sv0[2], ssv), i = dequant4_bf16(sv0[3], ssv);
-      dv[0] = make_uint4(e.x, e.y, f.x, f.y);
-      dv[1] = make_uint4(g.x, g.y, i.x, i.y);
+      out[2] = make_uint4(e.x, e.y, f.x, f.y);
+      out[3] = make_uint4(g.x, g.y, i.x, i.y);
     }
+  };
+  auto write_tile = [&](int buf, const uint4* v) {
+    uint4* dk = reinterpret_cast<uint4*>(lds + buf * STAGE + skey * KP + schunk * 32);
+    uint4* dv = reinterpret_cast<uint4*>(lds + buf * STAGE + K_TILE + skey * VP + schunk * 32);
+    dk[0] = v[0];
+    dk[1] = v[1];
+    dv[0] = v[2];
+    dv[1] = v[3];
+  };
+  auto store_tile = [&](int buf) {
+    uint4 v[4];
+    dequant_tile(v);
+    write_tile(buf, v);
   };
 
   // ---- Q^T fragments for this wave's 32 queries (kept for the whole kernel)
@@ -252,52 +304,73 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   float l_run = 0.f;        // this half's row sum (its 32 of every 64 keys)
 
   const int n_tiles = (p.n_kv + BKV - 1) / BKV;
-  load_tile(0);
-  store_tile(0);
-  if (n_tiles > 1) load_tile(BKV);
-  __syncthreads();
 
-  for (int it = 0; it < n_tiles; ++it) {
+  // One tile: scores with the staging of the next tile (into the other stage,
+  // freed by the last barrier) and the loads of the one after; the column
+  // max and the rare rescale; then the exponentials with O^T += V^T P^T.
+  // Straight-line apart from the rescale: tiles past the end load as zeros
+  // and land in the stage nobody reads any more; the last tile is peeled for
+  // the masking of keys past n_kv.
+  auto body = [&](int it, auto LAST) {
     const int cur = it & 1;
     const uint8_t* st = lds + cur * STAGE;
 
-    // S^T = K Q^T for 2 blocks of 32 keys
+    // K fragments of the tile, all in flight before the first MFMA.
+    v8bf kf[2][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        kf[b][ks] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(st + k_lane + b * 32 * KP + ks * 32));
+    // S^T = K Q^T for 2 blocks of 32 keys, with the next tile's dequantization
+    // (registers only) between the MFMAs.
+    uint4 nxt[4];
+    dequant_tile(nxt);
     v16f s[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) s[b] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const v8bf kf = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(st + k_lane + b * 32 * KP + ks * 32));
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[b], 0, 0, 0);
+      for (int b = 0; b < 2; ++b) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[b][ks], qf[ks], s[b], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the 16 K-fragment reads first
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // then 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // and 5 VALU, alternating
+    }
+    // the next tile into the other stage (freed by the last barrier), the
+    // loads of the one after, and this tile's V^T operands (in flight
+    // during the softmax).
+    write_tile(cur ^ 1, nxt);
+    load_tile((it + 2) * BKV);
+    v8bf vf[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint8_t* va = st + v_lane + (16 * t) * VP + db * 64;
+        const v4s lo = read_tr(va);
+        const v4s hi = read_tr(va + 8 * VP);
+        vf[t][db] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
-    }
 
-    // Next tile into the other stage (its previous tile finished before the
-    // barrier that ended the last iteration), then the loads of the one after.
-    if (it + 1 < n_tiles) {
-      store_tile(cur ^ 1);
-      if (it + 2 < n_tiles) load_tile((it + 2) * BKV);
-    }
-
-    // Keys past n_kv (last tile only) are excluded.
-    const int key_base = it * BKV;
-    if (key_base + BKV > p.n_kv) {
+    if constexpr (decltype(LAST)::value) {
+      const int key_base = it * BKV;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (key_base + b * 32 + g * 8 + half * 4 + e >= p.n_kv) s[b][4 * g + e] = -INFINITY;
+            s[b][4 * g + e] = key_base + b * 32 + g * 8 + half * 4 + e >= p.n_kv ? -INFINITY : s[b][4 * g + e];
     }
     float mt = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[b][e]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = pair_max(mt);
     // exponents in base 2: p = 2^(c * (s - m_use)), c = softmax_scale * log2(e) >= 0
     if (__ballot(mt > m_thr)) {
       const float m_new = fmaxf(m_use, mt);
@@ -310,8 +383,8 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       neg_mc = (m_new == -INFINITY) ? 0.f : -m_new * c;
     }
     // P for 16-key step t (keys 16t..16t+15 of the tile): elements 0-3 are
-    // keys 4 half + 0..3, elements 4-7 keys 8 + 4 half + 0..3.
-    v8bf pf[4];
+    // keys 4 half + 0..3, elements 4-7 keys 8 + 4 half + 0..3; each step's
+    // P feeds its 4 PV MFMAs (O^T += V^T P^T: 4 blocks of 32 d).
     float ls[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -324,28 +397,26 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       }
       const uint32_t w0 = cvt_bf16x2(pv[0], pv[1]), w1 = cvt_bf16x2(pv[2], pv[3]);
       const uint32_t w2 = cvt_bf16x2(pv[4], pv[5]), w3 = cvt_bf16x2(pv[6], pv[7]);
-      pf[t] = __builtin_bit_cast(v8bf, make_uint4(w0, w1, w2, w3));
+      const v8bf pf = __builtin_bit_cast(v8bf, make_uint4(w0, w1, w2, w3));
       ls[t] = add_bf16x2(w3, add_bf16x2(w2, add_bf16x2(w1, add_bf16x2(w0, 0.f))));
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t][db], pf, o[db], 0, 0, 0);
     }
     l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-
-    // O^T += V^T P^T : 4 blocks of 32 d, 4 steps of 16 keys
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const uint8_t* va = st + v_lane + (16 * t) * VP + db * 64;
-        const v4s lo = read_tr(va);
-        const v4s hi = read_tr(va + 8 * VP);
-        const v8bf vf = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t], o[db], 0, 0, 0);
-      }
-    }
     __syncthreads();
+  };
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+    load_tile(BKV);
+    __syncthreads();
+    for (int it = 0; it + 1 < n_tiles; ++it) body(it, std::false_type{});
+    body(n_tiles - 1, std::true_type{});
   }
 
   // normalize and store: lane's query q, d = 32*db + 8*(r/4) + 4*half + r%4
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   const int q = q0 + wave * 32 + l32;
   if (q < p.Lq) {
