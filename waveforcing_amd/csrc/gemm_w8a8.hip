@@ -133,12 +133,14 @@ struct GemmArgs {
   int vec16;             // y and ldy allow 16-byte row stores
 };
 
-// GELU(approximate='tanh') with tanh(u) = 1 - 2 / (1 + e^{2u}) on the
-// hardware exponential: absolute error ~1e-7 against tanhf.
+// GELU(approximate='tanh'): 0.5 x (1 + tanh(u)) = x / (1 + e^{-2u}) with
+// u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as x * rcp(1 + 2^{-2u log2 e})
+// on the hardware exponential and reciprocal (relative error ~3e-7 against
+// the tanh form; x -> -inf gives -0, x -> +inf gives x).
 __device__ inline float gelu_tanh(float x) {
-  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  const float t = 1.0f - 2.0f / (1.0f + __expf(2.0f * u));
-  return 0.5f * x * (1.0f + t);
+  const float inner = x * fmaf(0.044715f, x * x, 1.0f);     // x + 0.044715 x^3
+  const float e = __builtin_amdgcn_exp2f(-2.3022082f * inner);  // 2 sqrt(2/pi) log2(e) = 2.3022082
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 template <typename OP, bool HAS_BIAS, bool GELU>
