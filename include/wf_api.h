@@ -87,6 +87,44 @@ int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens,
                    float* k_scales, float* v_scales, int64_t pool_pages,
                    void* stream);
 
+/* wf_fp8_kv_pack with K rotated first: each head's interleaved pairs
+ * (k[2i], k[2i+1]) of token t become (a c - b s, a s + b c) in fp32 with
+ * c = cos[t][i], s = sin[t][i] (fp32 [n_tokens][head_dim / 2], 16-byte
+ * aligned), rounded to bf16, and the rounded values are quantized.  V is
+ * packed unrotated.  The anchor re-RoPE of the exchange and its slot copy in
+ * one pass: _anchor_working's _apply_rotary_emb(ku, cos, sin,
+ * is_neox_style=False).type_as(v) (wave_rt/denoiser/exchange/common.py:70-91)
+ * followed by Kb[off:off + T].copy_(ak) (paged.py:222-227). */
+int wf_fp8_kv_pack_rope(const void* k, const void* v, int64_t n_tokens,
+                        int32_t n_heads, int32_t head_dim, int64_t ld_kv,
+                        const float* cos, const float* sin,
+                        const int32_t* page_table, int64_t n_table,
+                        int32_t page_tokens, uint8_t* k_codes,
+                        uint8_t* v_codes, float* k_scales, float* v_scales,
+                        int64_t pool_pages, void* stream);
+
+/* K straight from the fused QKV output into the pages: per token,
+ * y = bf16(bf16(k * rsqrt(mean(k^2) + eps)) * norm_w) over the full row of
+ * n_heads * head_dim values (as wf_rmsnorm_rope), stored to ku_out (bf16,
+ * row stride ld_ku; may be K itself with ld_ku == ld_kv, or NULL) before the
+ * rotation, rotated by cos/sin as in wf_fp8_kv_pack_rope (NULL: no
+ * rotation), and packed; V (NULL: K only) is packed as by wf_fp8_kv_pack.
+ * Results equal wf_rmsnorm_rope followed by wf_fp8_kv_pack, bit for bit.
+ * n_heads * head_dim <= 16384.  Replaces norm_k (naive_rt/rolling_forcing/
+ * wan/modules/causal_model.py:112-116), the key RoPE of the patched forward
+ * (wave_rt/runtime/backend.py:119-121) and the self-slot publish/copy of
+ * the paged exchange (wave_rt/denoiser/exchange/paged.py:206-237); ku_out
+ * keeps the un-rotated key the exchange passes as unroped_key (backend.py:
+ * 122-133) for a later anchor re-RoPE. */
+int wf_k_norm_rope_kv_pack(const void* k, const void* v, int64_t n_tokens,
+                           int32_t n_heads, int32_t head_dim, int64_t ld_kv,
+                           float eps, const void* norm_w, const float* cos,
+                           const float* sin, void* ku_out, int64_t ld_ku,
+                           const int32_t* page_table, int64_t n_table,
+                           int32_t page_tokens, uint8_t* k_codes,
+                           uint8_t* v_codes, float* k_scales, float* v_scales,
+                           int64_t pool_pages, void* stream);
+
 /* Gather + dequantize the first n_tokens logical tokens of the pools back to
  * bf16 [n_tokens][n_heads][head_dim]: out = bf16_rne(float(code) * s).
  * `v_*` may be NULL to unpack K only.  Replaces the dequant of

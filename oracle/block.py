@@ -68,6 +68,25 @@ def rope_apply(x, angles):
     return torch.view_as_real(xc * rot).flatten(2).to(x.dtype)
 
 
+def rope_apply_table(x, cos, sin):
+    """x [T, H, D] bf16 rotated by fp32 tables cos/sin [T, D/2] -> bf16.
+
+    The table form of the same rotation, as the exchange applies it with
+    SGLang's precomputed cos/sin (_anchor_rope / _apply_rotary_emb with
+    is_neox_style=False, wave_rt/denoiser/exchange/common.py:45-91,
+    backend.py:119-121): pair (a, b) = (x[2i], x[2i+1]) becomes
+    (a*c - b*s, a*s + b*c), each product, difference and sum an fp32 operation,
+    then rounded once to bf16.
+    """
+    T, H, D = x.shape
+    xf = x.float().reshape(T, H, D // 2, 2)
+    a, b = xf[..., 0], xf[..., 1]
+    c = cos.float().view(T, 1, D // 2)
+    s = sin.float().view(T, 1, D // 2)
+    out = torch.stack((a * c - b * s, a * s + b * c), dim=-1)
+    return out.reshape(T, H, D).to(torch.bfloat16)
+
+
 def block_forward(p, x, e, grid, start_frame, pool_k, pool_v, context_table, own_table, n_context, page_tokens,
                   text_k, text_v, heads):
     """One block on the CPU.

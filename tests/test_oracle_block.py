@@ -6,11 +6,17 @@
   rotations preserve each pair's norm, and the angle table equals the host
   table generator's (waveforcing_amd.rope, written separately);
 - the norms match torch's layer_norm / the closed-form RMS definition in
-  float64.
+  float64;
+- the table form of RoPE (fp32 cos/sin, fp32 arithmetic, one bf16 rounding)
+  agrees with the float64 complex rotation to one bf16 ulp and exactly in
+  all but a few near-tie elements, is exact for the rotations by 0, 90 and
+  180 degrees, and equals a scalar numpy-float32 evaluation element by
+  element.
 """
 
 import dataclasses
 
+import numpy as np
 import torch
 
 from oracle import block as ob
@@ -60,3 +66,56 @@ def test_norms_match_definitions():
     assert torch.allclose(ob.layer_norm(x).double(), ln, rtol=2 ** -7, atol=1e-2)
     rms = xd / torch.sqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6) * w.double()
     assert torch.allclose(ob.rms_norm(x, w).double(), rms, rtol=2 ** -6, atol=1e-2)
+
+
+def _bf16_ulp(x):
+    e = torch.floor(torch.log2(x.abs().clamp(min=2.0 ** -126)))
+    return torch.pow(2.0, e - 7)
+
+
+def test_rope_table_form_matches_float64_rotation():
+    g = torch.Generator().manual_seed(5)
+    ang = ob.rope_angles(3, 6, 7, 11)
+    T = ang.shape[0]
+    x = torch.randn((T, 3, 128), generator=g).to(torch.bfloat16)
+    cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    got = ob.rope_apply_table(x, cos, sin).double()
+    want = ob.rope_apply(x, ang).double()
+    diff = (got - want).abs()
+    assert (diff <= _bf16_ulp(want) + 1e-30).all()
+    assert (diff > 0).double().mean() < 0.02
+    # a half-split (neox) pairing or a flipped sine sign is far off
+    assert (ob.rope_apply_table(x, cos, -sin).double() - want).abs().max() > 0.5
+
+
+def test_rope_table_form_special_rotations():
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn((5, 2, 128), generator=g).to(torch.bfloat16)
+    one, zero = torch.ones((5, 64)), torch.zeros((5, 64))
+    assert torch.equal(ob.rope_apply_table(x, one, zero), x)
+    assert torch.equal(ob.rope_apply_table(x, -one, zero), -x)
+    r90 = ob.rope_apply_table(x, zero, one).reshape(5, 2, 64, 2)
+    xp = x.reshape(5, 2, 64, 2)
+    assert torch.equal(r90[..., 0], -xp[..., 1]) and torch.equal(r90[..., 1], xp[..., 0])
+
+
+def test_rope_table_form_equals_scalar_float32():
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn((4, 1, 128), generator=g).to(torch.bfloat16)
+    ang = torch.rand((4, 64), generator=g, dtype=torch.float64) * 100
+    cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    got = ob.rope_apply_table(x, cos, sin).float().numpy()
+    xf = x.float().numpy()
+    c, s = cos.numpy(), sin.numpy()
+
+    def bf16(v):  # round-to-nearest-even of a float32 to bf16, as float32
+        u = np.array([v], dtype=np.float32).view(np.uint32)[0]
+        u = (int(u) + 0x7FFF + ((int(u) >> 16) & 1)) & 0xFFFF0000
+        return np.array([u], dtype=np.uint32).view(np.float32)[0]
+
+    for t in range(4):
+        for i in range(64):
+            a, b = np.float32(xf[t, 0, 2 * i]), np.float32(xf[t, 0, 2 * i + 1])
+            ci, si = np.float32(c[t, i]), np.float32(s[t, i])
+            assert got[t, 0, 2 * i] == bf16(np.float32(a * ci) - np.float32(b * si))
+            assert got[t, 0, 2 * i + 1] == bf16(np.float32(a * si) + np.float32(b * ci))

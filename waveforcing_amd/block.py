@@ -7,7 +7,8 @@ WaveRT's SGLang model runs (F4 of the path's survey), with:
 * every block linear W8A8 int8 (the ``scope=all`` swap of
   wave_rt/runtime/fp8.py:93-137, per-token / per-channel int8);
 * norm + modulation + activation quantization fused into one row kernel;
-* q/k RMSNorm + 3-D RoPE fused into one row kernel;
+* q RMSNorm + 3-D RoPE fused into one row kernel; K's RMSNorm + RoPE + FP8
+  pack and V's pack fused into another, straight from the QKV output;
 * self-attention over the FP8 paged context: this chunk's K/V are packed
   into its pages, then attention reads the prior chunks' pages plus its own
   (the single-GPU form of the paged exchange, paged.py:206-247);
@@ -211,7 +212,8 @@ class QuantizedWanBlock:
         return kn.view(L, self.heads, self.head_dim), v.view(L, self.heads, self.head_dim)
 
     def forward(self, x: torch.Tensor, e: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pool: Fp8PagePool,
-                context_table: PageTable, own_table: PageTable, n_context: int, text_kv) -> torch.Tensor:
+                context_table: PageTable, own_table: PageTable, n_context: int, text_kv,
+                unroped_k_out: torch.Tensor | None = None) -> torch.Tensor:
         """Advance x [T, dim] bf16 in place through the block.
 
         e: [F, 6, dim] bf16 time modulation of the chunk's F frames.
@@ -219,6 +221,8 @@ class QuantizedWanBlock:
         pool/context_table/n_context: this layer's FP8 page context (prior
         chunks' pages followed by ``own_table``'s pages), of n_context keys
         including this chunk's T tokens, which are packed into own_table here.
+        unroped_k_out: optional [T, dim] bf16 buffer for this chunk's normalized,
+        un-rotated K (the exchange's unroped_key, kept for the anchor re-RoPE).
         """
         T, dim = x.shape
         F = e.shape[0]
@@ -240,8 +244,8 @@ class QuantizedWanBlock:
         q, k, v = qkv[:, :dim], qkv[:, dim:2 * dim], qkv[:, 2 * dim:]
         # in place: each row is read whole before its reduction, written after
         _rmsnorm_rope(q, hd, self.norm_q, cos, sin, q)
-        _rmsnorm_rope(k, hd, self.norm_k, cos, sin, k)
-        pool.pack(k.view(T, H, hd), v.view(T, H, hd), own_table)
+        # K: RMSNorm + RoPE + FP8 pack into this chunk's pages, V packed beside it
+        pool.pack_k_norm_rope(k, v, own_table, self.norm_k, EPS, (cos, sin), ku_out=unroped_k_out)
         ctx = PagedKV(pool, context_table, n_context)
         attn_paged_fp8(q.view(T, H, hd), ctx, out=ws["attn"].view(T, H, hd))
         _linear_i8(ws["attn"], self.o, aq, as_, ws["y"])

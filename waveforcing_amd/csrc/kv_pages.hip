@@ -23,8 +23,22 @@
 // quotient of two 8-bit significands is either exact (and the residual step
 // returns it exactly) or at least 2^-14 (relative) away from every e4m3
 // rounding boundary, so the code equals that of the IEEE quotient.
+//
+// Two fused producers feed the same pages:
+// * kv_pack_kernel<..., ROPE = true> rotates K by a per-token RoPE table
+//   before quantizing it: the anchor re-RoPE of the exchange
+//   (wave_rt/denoiser/exchange/common.py:70-91), whose rotated bf16 K the
+//   reference copies into slot 0 (paged.py:222-227), packed in one pass;
+// * k_norm_rope_pack_kernel takes K straight from the fused QKV output:
+//   RMSNorm over the token's full row, RoPE, FP8 pack, and V's pack, one
+//   token row per wave or workgroup (the row engine of rows.hpp).
+// The rotation of a pair (a, b) by angle i is (a c - b s, a s + b c) in fp32
+// with the table's fp32 cos/sin (the library is built without FMA
+// contraction), rounded to bf16 before the quantization, as the reference
+// rounds the rotated K to bf16 (`.type_as(v)`, common.py:86-88).
 #include "fastdiv.hpp"
 #include "fp8_codec.hpp"
+#include "rows.hpp"
 #include "wf_common.hpp"
 
 namespace wf {
@@ -81,8 +95,8 @@ __device__ inline bool locate(const PageGeom& g, uint32_t r, int64_t& code_row, 
   return true;
 }
 
-__device__ inline uint32_t quant4(uint32_t w01, uint32_t w23, float s, float r) {
-  const float x[4] = {bf16_lo_to_f32(w01), bf16_hi_to_f32(w01), bf16_lo_to_f32(w23), bf16_hi_to_f32(w23)};
+// Four e4m3 codes of bf16-exact values x[0..3] with scale s (r = RN(1/s)).
+__device__ inline uint32_t quant4f(const float* x, float s, float r) {
   float q[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -94,6 +108,32 @@ __device__ inline uint32_t quant4(uint32_t w01, uint32_t w23, float s, float r) 
     q[i] = bits_f32(f32_bits(qi) | (f32_bits(x[i]) & 0x80000000u));
   }
   return e4m3_pack4_hw(q[0], q[1], q[2], q[3]);
+}
+
+__device__ inline uint32_t quant4(uint32_t w01, uint32_t w23, float s, float r) {
+  const float x[4] = {bf16_lo_to_f32(w01), bf16_hi_to_f32(w01), bf16_lo_to_f32(w23), bf16_hi_to_f32(w23)};
+  return quant4f(x, s, r);
+}
+
+// Rotate the 4 pairs of 8 fp32 values by (c[j], s[j]) and round to bf16.
+__device__ inline void rope4_bf16(float* y, const float4& c4, const float4& s4) {
+  const float cs[4] = {c4.x, c4.y, c4.z, c4.w};
+  const float sn[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float x0 = y[2 * j], x1 = y[2 * j + 1];
+    y[2 * j] = x0 * cs[j] - x1 * sn[j];
+    y[2 * j + 1] = x0 * sn[j] + x1 * cs[j];
+  }
+  rows::rbf8(y);
+}
+
+// The same on a 16-byte chunk of 8 bf16 values.
+__device__ inline uint4 rope_chunk(const uint4& w, const float4& c4, const float4& s4) {
+  float y[8];
+  rows::unpack8(w, y);
+  rope4_bf16(y, c4, s4);
+  return rows::pack8(y);
 }
 
 __device__ inline float absmax8(const uint4& a, const uint4& b) {
@@ -131,11 +171,13 @@ __device__ inline void st16(uint4* p, const uint4& v) {
   }
 }
 
-template <bool NT_LOAD, bool NT_STORE>
+// ROPE: K rows are rotated by the token's row of cos/sin [n_tokens][64] first.
+template <bool NT_LOAD, bool NT_STORE, bool ROPE>
 __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ k, const uint4* __restrict__ v,
                                                       int64_t ld_kv, uint32_t n_rows, uint32_t n_blocks,
                                                       uint32_t n_items, PageGeom geom, PoolView kpool,
-                                                      PoolView vpool) {
+                                                      PoolView vpool, const float* __restrict__ cos,
+                                                      const float* __restrict__ sin) {
   uint32_t blk;
   bool is_v;
   if (!block_of(n_blocks, n_items, blk, is_v)) return;
@@ -151,6 +193,15 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ 
     const uint4* p = src + (static_cast<int64_t>(t) * ld_kv + h * kHeadDim) / 8 + lane8 * 2;
     a = ld16<NT_LOAD>(p);
     b = ld16<NT_LOAD>(p + 1);
+    if constexpr (ROPE) {
+      if (!is_v) {
+        // pairs 8 lane8 .. 8 lane8 + 7 of the head
+        const float4* cp = reinterpret_cast<const float4*>(cos + static_cast<int64_t>(t) * (kHeadDim / 2)) + lane8 * 2;
+        const float4* sp = reinterpret_cast<const float4*>(sin + static_cast<int64_t>(t) * (kHeadDim / 2)) + lane8 * 2;
+        a = rope_chunk(a, cp[0], sp[0]);
+        b = rope_chunk(b, cp[1], sp[1]);
+      }
+    }
   }
   // every lane of the 8-lane group takes part in the reduction
   const float amax = group8_max(absmax8(a, b));
@@ -165,6 +216,124 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ 
   if (r < n_rows && locate(geom, r, code_row, scale_idx)) {
     st16<NT_STORE>(reinterpret_cast<uint4*>(pool.codes + code_row * kHeadDim) + lane8, c);
     if (lane8 == 0) pool.scales[scale_idx] = s;
+  }
+}
+
+// ------------------------------------------- K RMSNorm + RoPE + K/V pack
+struct KNormPackArgs {
+  const uint16_t* k;    // bf16 [T][ld_kv]: n_heads * 128 values per token
+  const uint16_t* v;    // bf16 [T][ld_kv] or null
+  int64_t ld_kv;
+  int T;
+  float eps;
+  const uint16_t* w;    // RMSNorm weight [n_heads * 128] bf16
+  const float* cos;     // [T][64] or null (no rotation)
+  const float* sin;
+  uint16_t* ku;         // normalized, un-rotated K [T][ld_ku] bf16, or null
+  int64_t ld_ku;
+  PageGeom geom;
+  PoolView kpool, vpool;
+};
+
+// Page position of token t: code row of head 0 and scale index of head 0
+// (head h adds h * 128 codes and h * page_tokens scales).  False when the
+// token's logical page has no valid physical page.
+__device__ inline bool token_slot(const PageGeom& g, uint32_t t, int64_t& code_row0, int64_t& scale0) {
+  uint32_t lp, rip;
+  g.page.divmod(t, lp, rip);
+  if (lp >= g.n_table) return false;
+  const int32_t page = g.table[lp];
+  if (page < 0 || page >= g.pool_pages) return false;
+  code_row0 = (static_cast<int64_t>(page) * g.page_tokens + rip) * g.n_heads;
+  scale0 = static_cast<int64_t>(page) * g.n_heads * g.page_tokens + rip;
+  return true;
+}
+
+// Quantize the 8 bf16-exact values y of chunk ch (head ch / 16) with the
+// head's scale, which the 16 lanes holding that head reduce together, and
+// store 8 codes (+ the scale from the head's first lane).
+__device__ inline void pack_head_chunk(const float* y, int ch, bool valid, bool placed, const PageGeom& g,
+                                       int64_t code_row0, int64_t scale0, const PoolView& pool) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(y[i]));
+  const float amax = rows::group16_max(m);
+  const float s = scale_from_amax(amax);
+  const float r = __frcp_rn(s);
+  const uint2 c = make_uint2(quant4f(y, s, r), quant4f(y + 4, s, r));
+  if (valid && placed) {
+    const int h = ch >> 4;
+    *reinterpret_cast<uint2*>(pool.codes + (code_row0 + h) * kHeadDim + (ch & 15) * 8) = c;
+    if ((ch & 15) == 0) pool.scales[scale0 + static_cast<int64_t>(h) * g.page_tokens] = s;
+  }
+}
+
+// One token row per LPR lanes (rows.hpp): K = RMSNorm(k) over the row
+// (y = bf16(bf16(k * rsqrt(mean(k^2) + eps)) * w), WanRMSNorm, model.py:78-86,
+// with the reduction of rmsnorm_rope_kernel), optionally stored un-rotated,
+// then rotated per head and packed; V packed as is.  Lane chunk ch covers
+// elements 8 ch .. 8 ch + 7, so a head's 16 chunks sit in 16 aligned lanes.
+template <int LPR, int NC>
+__global__ __launch_bounds__(256) void k_norm_rope_pack_kernel(KNormPackArgs a) {
+  constexpr int RPB = 256 / LPR;
+  __shared__ float red[4];
+  const int lane = static_cast<int>(threadIdx.x) % LPR;
+  const int t = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / LPR;
+  if (t >= a.T) return;
+  const int n_chunks = static_cast<int>(a.geom.n_heads) * (kHeadDim / 8);
+  const uint16_t* krow = a.k + static_cast<int64_t>(t) * a.ld_kv;
+  float x[NC][8];
+  uint4 vw[NC];
+  float sq = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ch = lane + LPR * c;
+    rows::unpack8(ch < n_chunks ? rows::ld16(krow + ch * 8) : make_uint4(0, 0, 0, 0), x[c]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sq += x[c][i] * x[c][i];
+  }
+  if (a.v) {
+    const uint16_t* vrow = a.v + static_cast<int64_t>(t) * a.ld_kv;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int ch = lane + LPR * c;
+      vw[c] = ch < n_chunks ? rows::ld16(vrow + ch * 8) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  int64_t code_row0 = 0, scale0 = 0;
+  const bool placed = token_slot(a.geom, static_cast<uint32_t>(t), code_row0, scale0);
+  const float ms = rows::row_sum<LPR>(sq, red) / static_cast<float>(n_chunks * 8);
+  const float rn = 1.0f / sqrtf(ms + a.eps);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ch = lane + LPR * c;
+    const bool valid = ch < n_chunks;
+    float wv[8];
+    rows::unpack8(valid ? rows::ld16(a.w + ch * 8) : make_uint4(0, 0, 0, 0), wv);
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = x[c][i] * rn;
+    rows::rbf8(y);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = y[i] * wv[i];
+    rows::rbf8(y);
+    if (a.ku && valid) rows::st16(a.ku + static_cast<int64_t>(t) * a.ld_ku + ch * 8, rows::pack8(y));
+    if (a.cos) {
+      const int64_t p0 = static_cast<int64_t>(t) * (kHeadDim / 2) + (ch & 15) * 4;  // first pair of the chunk
+      const float4 c4 = valid ? *reinterpret_cast<const float4*>(a.cos + p0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 s4 = valid ? *reinterpret_cast<const float4*>(a.sin + p0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      rope4_bf16(y, c4, s4);
+    }
+    pack_head_chunk(y, ch, valid, placed, a.geom, code_row0, scale0, a.kpool);
+  }
+  if (a.v) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int ch = lane + LPR * c;
+      float y[8];
+      rows::unpack8(vw[c], y);
+      pack_head_chunk(y, ch, ch < n_chunks, placed, a.geom, code_row0, scale0, a.vpool);
+    }
   }
 }
 
@@ -235,6 +404,40 @@ PageGeom make_geom(int32_t n_heads, const int32_t* page_table, int64_t n_table, 
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// wf_fp8_kv_pack and wf_fp8_kv_pack_rope (cos/sin null: no rotation).
+int launch_pack(const char* fn, const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
+                int64_t ld_kv, const float* cos, const float* sin, const int32_t* page_table, int64_t n_table,
+                int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales, float* v_scales,
+                int64_t pool_pages, void* stream) {
+  if (int st = check_pool_args(fn, n_tokens, n_heads, head_dim, page_table, n_table, page_tokens, pool_pages))
+    return st;
+  if (n_tokens == 0) return WF_OK;
+  WF_REQUIRE(k && k_codes && k_scales, WF_E_INVALID, "%s: null K pointer", fn);
+  WF_REQUIRE(ld_kv >= static_cast<int64_t>(n_heads) * head_dim && ld_kv % 8 == 0, WF_E_INVALID,
+             "%s: ld_kv=%lld must be >= n_heads*head_dim and a multiple of 8", fn, (long long)ld_kv);
+  const bool has_v = v != nullptr;
+  WF_REQUIRE(!has_v || (v_codes && v_scales), WF_E_INVALID, "%s: V given without V pool", fn);
+  WF_REQUIRE(aligned16(k) && aligned16(k_codes) && (!has_v || (aligned16(v) && aligned16(v_codes))), WF_E_ALIGN,
+             "%s: K/V and code pools must be 16-byte aligned", fn);
+  const uint32_t n_rows = static_cast<uint32_t>(n_tokens * n_heads);
+  const PageGeom geom = make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
+  const uint32_t n_blocks = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const uint32_t items = has_v ? 2 * n_blocks : n_blocks;
+  const dim3 grid((items + kNumXcd - 1) / kNumXcd * kNumXcd);
+  const uint4* k4 = reinterpret_cast<const uint4*>(k);
+  const uint4* v4 = reinterpret_cast<const uint4*>(v);
+  if (cos) {
+    hipLaunchKernelGGL((kv_pack_kernel<kPackNtLoad, kPackNtStore, true>), grid, dim3(256), 0, as_stream(stream), k4,
+                       v4, ld_kv, n_rows, n_blocks, items, geom, PoolView{k_codes, k_scales},
+                       PoolView{v_codes, v_scales}, cos, sin);
+  } else {
+    hipLaunchKernelGGL((kv_pack_kernel<kPackNtLoad, kPackNtStore, false>), grid, dim3(256), 0, as_stream(stream), k4,
+                       v4, ld_kv, n_rows, n_blocks, items, geom, PoolView{k_codes, k_scales},
+                       PoolView{v_codes, v_scales}, nullptr, nullptr);
+  }
+  return check_launch(fn);
+}
+
 }  // namespace
 }  // namespace wf
 
@@ -243,25 +446,77 @@ extern "C" {
 int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
                    int64_t ld_kv, const int32_t* page_table, int64_t n_table, int32_t page_tokens, uint8_t* k_codes,
                    uint8_t* v_codes, float* k_scales, float* v_scales, int64_t pool_pages, void* stream) {
-  static const char* fn = "wf_fp8_kv_pack";
+  return wf::launch_pack("wf_fp8_kv_pack", k, v, n_tokens, n_heads, head_dim, ld_kv, nullptr, nullptr, page_table,
+                         n_table, page_tokens, k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
+}
+
+int wf_fp8_kv_pack_rope(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
+                        int64_t ld_kv, const float* cos, const float* sin, const int32_t* page_table, int64_t n_table,
+                        int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales, float* v_scales,
+                        int64_t pool_pages, void* stream) {
+  static const char* fn = "wf_fp8_kv_pack_rope";
+  WF_REQUIRE(n_tokens == 0 || (cos && sin), WF_E_INVALID, "%s: null RoPE table", fn);
+  WF_REQUIRE(wf::aligned16(cos) && wf::aligned16(sin), WF_E_ALIGN, "%s: RoPE tables must be 16-byte aligned", fn);
+  return wf::launch_pack(fn, k, v, n_tokens, n_heads, head_dim, ld_kv, cos, sin, page_table, n_table, page_tokens,
+                         k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
+}
+
+int wf_k_norm_rope_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
+                           int64_t ld_kv, float eps, const void* norm_w, const float* cos, const float* sin,
+                           void* ku_out, int64_t ld_ku, const int32_t* page_table, int64_t n_table,
+                           int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales, float* v_scales,
+                           int64_t pool_pages, void* stream) {
+  static const char* fn = "wf_k_norm_rope_kv_pack";
   if (int st = wf::check_pool_args(fn, n_tokens, n_heads, head_dim, page_table, n_table, page_tokens, pool_pages))
     return st;
   if (n_tokens == 0) return WF_OK;
-  WF_REQUIRE(k && k_codes && k_scales, WF_E_INVALID, "%s: null K pointer", fn);
-  WF_REQUIRE(ld_kv >= static_cast<int64_t>(n_heads) * head_dim && ld_kv % 8 == 0, WF_E_INVALID,
-             "%s: ld_kv=%lld must be >= n_heads*head_dim and a multiple of 8", fn, (long long)ld_kv);
-  const bool has_v = v != nullptr;
-  WF_REQUIRE(!has_v || (v_codes && v_scales), WF_E_INVALID, "%s: V given without V pool", fn);
-  WF_REQUIRE(wf::aligned16(k) && wf::aligned16(k_codes) && (!has_v || (wf::aligned16(v) && wf::aligned16(v_codes))),
-             WF_E_ALIGN, "%s: K/V and code pools must be 16-byte aligned", fn);
-  const uint32_t n_rows = static_cast<uint32_t>(n_tokens * n_heads);
-  const wf::PageGeom geom = wf::make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
-  const uint32_t n_blocks = (n_rows + wf::kRowsPerBlock - 1) / wf::kRowsPerBlock;
-  const uint32_t items = has_v ? 2 * n_blocks : n_blocks;
-  const dim3 grid((items + wf::kNumXcd - 1) / wf::kNumXcd * wf::kNumXcd);
-  hipLaunchKernelGGL((wf::kv_pack_kernel<wf::kPackNtLoad, wf::kPackNtStore>), grid, dim3(256), 0,
-                     wf::as_stream(stream), reinterpret_cast<const uint4*>(k), reinterpret_cast<const uint4*>(v), ld_kv,
-                     n_rows, n_blocks, items, geom, wf::PoolView{k_codes, k_scales}, wf::PoolView{v_codes, v_scales});
+  const int64_t dim = static_cast<int64_t>(n_heads) * head_dim;
+  int lpr = 0, nc = 0;
+  WF_REQUIRE(wf::rows::pick_shape(dim / 8, lpr, nc), WF_E_SHAPE, "%s: n_heads*head_dim=%lld exceeds 16384", fn,
+             (long long)dim);
+  WF_REQUIRE(k && norm_w && k_codes && k_scales, WF_E_INVALID, "%s: null K, weight or K pool", fn);
+  WF_REQUIRE(!v || (v_codes && v_scales), WF_E_INVALID, "%s: V given without V pool", fn);
+  WF_REQUIRE((cos == nullptr) == (sin == nullptr), WF_E_INVALID, "%s: cos and sin must both be given or both null",
+             fn);
+  WF_REQUIRE(ld_kv >= dim && ld_kv % 8 == 0, WF_E_INVALID, "%s: ld_kv=%lld must be >= n_heads*head_dim and %% 8 == 0",
+             fn, (long long)ld_kv);
+  WF_REQUIRE(!ku_out || (ld_ku >= dim && ld_ku % 8 == 0), WF_E_INVALID, "%s: ld_ku must be >= n_heads*head_dim and "
+             "%% 8 == 0", fn);
+  WF_REQUIRE(wf::aligned16(k) && wf::aligned16(v) && wf::aligned16(norm_w) && wf::aligned16(cos) &&
+                 wf::aligned16(sin) && wf::aligned16(ku_out) && wf::aligned16(k_codes) && wf::aligned16(v_codes),
+             WF_E_ALIGN, "%s: tensors must be 16-byte aligned", fn);
+  if (ku_out) {
+    // in place over K (a lane rewrites only the chunks it has read) or disjoint from K and V
+    const uintptr_t kb = reinterpret_cast<uintptr_t>(k), ub = reinterpret_cast<uintptr_t>(ku_out);
+    const uintptr_t span_k = static_cast<uintptr_t>((n_tokens - 1) * ld_kv + dim) * 2;
+    const uintptr_t span_u = static_cast<uintptr_t>((n_tokens - 1) * ld_ku + dim) * 2;
+    const bool in_place = ub == kb && ld_ku == ld_kv;
+    WF_REQUIRE(in_place || ub + span_u <= kb || kb + span_k <= ub, WF_E_INVALID,
+               "%s: ku_out must be K itself (same stride) or not overlap it", fn);
+    if (v) {
+      const uintptr_t vb = reinterpret_cast<uintptr_t>(v);
+      WF_REQUIRE(ub + span_u <= vb || vb + span_k <= ub, WF_E_INVALID, "%s: ku_out overlaps V", fn);
+    }
+  }
+  wf::KNormPackArgs a;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.ld_kv = ld_kv;
+  a.T = static_cast<int>(n_tokens);
+  a.eps = eps;
+  a.w = static_cast<const uint16_t*>(norm_w);
+  a.cos = cos;
+  a.sin = sin;
+  a.ku = static_cast<uint16_t*>(ku_out);
+  a.ld_ku = ld_ku;
+  a.geom = wf::make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
+  a.kpool = wf::PoolView{k_codes, k_scales};
+  a.vpool = wf::PoolView{v_codes, v_scales};
+  const uint32_t grid = static_cast<uint32_t>((n_tokens + 256 / lpr - 1) / (256 / lpr));
+  wf::rows::dispatch_shape(lpr, nc, [&](auto L, auto C) {
+    hipLaunchKernelGGL((wf::k_norm_rope_pack_kernel<decltype(L)::value, decltype(C)::value>), dim3(grid), dim3(256),
+                       0, wf::as_stream(stream), a);
+  });
   return wf::check_launch(fn);
 }
 

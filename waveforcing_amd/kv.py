@@ -66,6 +66,15 @@ def _as_thd(x: torch.Tensor, name: str) -> torch.Tensor:
     return x
 
 
+def _rope_tables(rope, T: int, D: int, device):
+    cos, sin = rope
+    for name, t in (("cos", cos), ("sin", sin)):
+        on_device = t.device.type == device.type and (device.index is None or t.device.index == device.index)
+        if t.dtype != torch.float32 or tuple(t.shape) != (T, D // 2) or not t.is_contiguous() or not on_device:
+            raise ValueError(f"rope {name} must be contiguous fp32 [{T}, {D // 2}] on {device}")
+    return cos, sin
+
+
 class Fp8PagePool:
     """K and V page pools in HBM with pack / gather-dequant through the HIP kernels."""
 
@@ -101,8 +110,15 @@ class Fp8PagePool:
     def pages_for(self, n_tokens: int) -> int:
         return -(-n_tokens // self.page_tokens)
 
-    def pack(self, k: torch.Tensor, v: torch.Tensor | None, table: PageTable) -> None:
-        """Quantize K (and V) [T, H, D] bf16 into the pages listed by ``table``."""
+    def pack(self, k: torch.Tensor, v: torch.Tensor | None, table: PageTable,
+             rope: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
+        """Quantize K (and V) [T, H, D] bf16 into the pages listed by ``table``.
+
+        With ``rope = (cos, sin)`` (fp32 [T, D/2]), K is rotated first and the
+        rotated bf16 values are quantized: the anchor re-RoPE plus slot copy of
+        _anchor_working (wave_rt/denoiser/exchange/common.py:70-91,
+        paged.py:222-227) in one kernel.
+        """
         k = _as_thd(k, "k")
         if v is not None:
             v = _as_thd(v, "v")
@@ -118,9 +134,63 @@ class Fp8PagePool:
         if v is not None and (v.stride(0) if T > 1 else H * D) != ld:
             k, v = k.contiguous(), v.contiguous()
             ld = H * D
+        if rope is not None:
+            cos, sin = _rope_tables(rope, T, D, self.device)
+            _lib.call(
+                "wf_fp8_kv_pack_rope",
+                _lib.ptr(k), _lib.ptr(v), T, H, D, ld, cos.data_ptr(), sin.data_ptr(),
+                table.dev.data_ptr(), len(table), self.page_tokens,
+                self.k_codes.data_ptr(), self.v_codes.data_ptr() if v is not None else None,
+                self.k_scales.data_ptr(), self.v_scales.data_ptr() if v is not None else None,
+                self.pool_pages,
+                _lib.stream_handle(self.device),
+            )
+            return
         _lib.call(
             "wf_fp8_kv_pack",
             _lib.ptr(k), _lib.ptr(v), T, H, D, ld,
+            table.dev.data_ptr(), len(table), self.page_tokens,
+            self.k_codes.data_ptr(), self.v_codes.data_ptr() if v is not None else None,
+            self.k_scales.data_ptr(), self.v_scales.data_ptr() if v is not None else None,
+            self.pool_pages,
+            _lib.stream_handle(self.device),
+        )
+
+    def pack_k_norm_rope(self, k: torch.Tensor, v: torch.Tensor | None, table: PageTable, norm_w: torch.Tensor,
+                         eps: float, rope: tuple[torch.Tensor, torch.Tensor] | None,
+                         ku_out: torch.Tensor | None = None) -> None:
+        """K straight from the QKV projection into the pages.
+
+        k, v: [T, dim] bf16 rows (dim = H*D, token stride a multiple of 8, e.g.
+        column views of a fused QKV output).  K gets WanRMSNorm over the row
+        (norm_w [dim]), is written un-rotated to ``ku_out`` ([T, dim] bf16, may
+        be ``k`` itself) if given, is rotated by ``rope = (cos, sin)`` and is
+        packed; V is packed as by :meth:`pack`.  Equal, bit for bit, to
+        wf_rmsnorm_rope followed by wf_fp8_kv_pack.
+        """
+        for name, t in (("k", k), ("v", v), ("ku_out", ku_out)):
+            if t is None:
+                continue
+            if t.dim() != 2 or t.dtype != torch.bfloat16 or t.stride(1) != 1:
+                raise ValueError(f"{name} must be bf16 [T, dim] rows with unit column stride")
+        T, dim = k.shape
+        H, D = self.n_heads, self.head_dim
+        if dim != H * D:
+            raise ValueError(f"k rows have {dim} values; the pool holds {H} heads x {D}")
+        if v is not None and (tuple(v.shape) != (T, dim) or (T > 1 and v.stride(0) != k.stride(0))):
+            raise ValueError("v must match k's shape and token stride")
+        if ku_out is not None and tuple(ku_out.shape) != (T, dim):
+            raise ValueError("ku_out must be [T, dim]")
+        if len(table) * self.page_tokens < T:
+            raise RuntimeError(f"page table of {len(table)} pages cannot hold {T} tokens")
+        cos = sin = None
+        if rope is not None:
+            cos, sin = _rope_tables(rope, T, D, self.device)
+        ld = k.stride(0) if T > 1 else dim
+        _lib.call(
+            "wf_k_norm_rope_kv_pack",
+            k.data_ptr(), _lib.ptr(v), T, H, D, ld, float(eps), norm_w.data_ptr(), _lib.ptr(cos), _lib.ptr(sin),
+            _lib.ptr(ku_out), (ku_out.stride(0) if T > 1 else dim) if ku_out is not None else 0,
             table.dev.data_ptr(), len(table), self.page_tokens,
             self.k_codes.data_ptr(), self.v_codes.data_ptr() if v is not None else None,
             self.k_scales.data_ptr(), self.v_scales.data_ptr() if v is not None else None,
