@@ -247,6 +247,42 @@ def bench_block(scale: str, steps: int, warmup: int, dev: str):
     return {"ms": ms, "tokens": T, "context_keys": (prior + 1) * T}
 
 
+def bench_exchange(steps: int, warmup: int, dev: str):
+    """One denoise step's paged exchange over the 30 Wan-1.3B layers at steady state: per layer,
+    pack this chunk's K/V into its slot and re-RoPE + pack the anchor's K, with a full clean list
+    (anchor + 7) and a 24-frame window (anchor + 6 working chunks + self = 37440 keys)."""
+    from waveforcing_amd.exchange import CleanPage, PagedExchange
+
+    x = PagedExchange(LAYERS, HEADS, PAGE, frames_per_chunk=3, max_attn_frames=24, device=dev)
+    g = torch.Generator().manual_seed(21)
+    filler = torch.randn((TOKENS, HEADS, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    for layer in range(LAYERS):
+        for cid in range(8):
+            slot = x.reserve(layer)
+            x.pack(layer, slot, filler, filler)
+            x.append_clean(layer, CleanPage(cid, slot, ku=filler.clone() if cid == 0 else None))
+    k, v = inputs.kv_layer(0)
+    k, v = k.to(dev).unsqueeze(0), v.to(dev).unsqueeze(0)
+    n_ctx = []
+
+    def step():
+        exch = x.make_denoise_exch(8 * 3)
+        for layer in range(LAYERS):
+            ctx, _ = exch(layer_idx=layer, roped_query=None, roped_key=k, unroped_key=None, value=v,
+                          post_patch_height=30, post_patch_width=52)
+            if not n_ctx:
+                n_ctx.append(ctx.n_tokens)
+        x.finish_denoise()
+
+    ms = _timed(step, steps, warmup)
+    elems = TOKENS * HEADS * HEAD_DIM
+    rows = TOKENS * HEADS
+    anchor_bytes = elems * 2 + elems + rows * 4          # K only: read bf16, write codes + scales
+    layer_bytes = kv_bytes_per_layer() + anchor_bytes
+    return {"ms": ms, "us_per_layer": ms * 1e3 / LAYERS, "bytes_per_layer": layer_bytes,
+            "gbs": LAYERS * layer_bytes / (ms * 1e-3) / 1e9, "context_keys": n_ctx[0]}
+
+
 def bench_copy(steps: int, warmup: int, dev: str):
     """A plain device copy of 1 GiB (read 1 GiB + write 1 GiB): calibrates the HBM byte counters."""
     src = torch.empty((1 << 30,), dtype=torch.uint8, device=dev).fill_(1)
@@ -302,7 +338,7 @@ def main() -> None:
     ap.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
                     help="minimum untimed warm-up of the KV workloads (profiler runs use 0)")
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention",
-                                       "block_1p3b", "block_14b", "copy"],
+                                       "block_1p3b", "block_14b", "exchange_1p3b", "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -319,7 +355,7 @@ def main() -> None:
               "kv_unpack": lambda s, w, d: bench_kv(s, w, d, ("unpack",)), "gemm": bench_gemm,
               "linears_1p3b": bench_block_linears, "attention": bench_attention, "copy": bench_copy,
               "block_1p3b": lambda s, w, d: bench_block("1.3b", s, w, d),
-              "block_14b": lambda s, w, d: bench_block("14b", s, w, d)}[args.only]
+              "block_14b": lambda s, w, d: bench_block("14b", s, w, d), "exchange_1p3b": bench_exchange}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
     kv = bench_kv(args.steps, args.warmup, dev)
@@ -329,6 +365,7 @@ def main() -> None:
     at = at_sweep[8]
     b13 = bench_block("1.3b", max(5, args.steps // 5), 2, dev)
     b14 = bench_block("14b", max(3, args.steps // 10), 1, dev)
+    xch = bench_exchange(max(5, args.steps // 5), 2, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     # one launch per step: the launch duration is the step time
     achieved = kv["bytes_per_step"] / (kv["ms_pack"] * 1e-3) / 1e9
@@ -393,6 +430,11 @@ def main() -> None:
             "attn_paged_fp8_context_sweep": {f"{c}_chunks": {"keys": r["keys"], "ms": round(r["ms"], 4),
                                                               "tflops": round(r["tflops"], 1)}
                                              for c, r in at_sweep.items()},
+            "exchange_1p3b_us_per_layer": round(xch["us_per_layer"], 2),
+            "exchange_1p3b_gbs": round(xch["gbs"], 1),
+            "exchange_note": "denoise-side paged exchange per layer at steady state: this chunk's K/V packed into "
+                             "its slot + the anchor's K re-RoPEd and packed (65.4 MB algorithmic per layer); "
+                             "context anchor + 6 working + self = 37440 keys",
             "dit_block_1p3b_ms_per_chunk": round(b13["ms"], 4),
             "dit_block_14b_ms_per_chunk": round(b14["ms"], 4),
             "dit_block_note": "one block, 4680-token 3-frame chunk, 37440-key FP8 paged self-attn context, "

@@ -277,20 +277,29 @@ template <int LPR, int NC>
 __global__ __launch_bounds__(256) void k_norm_rope_pack_kernel(KNormPackArgs a) {
   constexpr int RPB = 256 / LPR;
   __shared__ float red[4];
+  // Row blocks go XCD-contiguously (as block_of), so the token-fastest scale
+  // lines of neighbouring tokens are written through one L2.
+  const uint32_t n_blk = (static_cast<uint32_t>(a.T) + RPB - 1) / RPB;
+  const uint32_t per_xcd = (n_blk + kNumXcd - 1) / kNumXcd;
+  const uint32_t blk = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
   const int lane = static_cast<int>(threadIdx.x) % LPR;
-  const int t = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / LPR;
-  if (t >= a.T) return;
+  const int t = static_cast<int>(blk) * RPB + static_cast<int>(threadIdx.x) / LPR;
+  if (blk >= n_blk || t >= a.T) return;
   const int n_chunks = static_cast<int>(a.geom.n_heads) * (kHeadDim / 8);
   const uint16_t* krow = a.k + static_cast<int64_t>(t) * a.ld_kv;
-  float x[NC][8];
-  uint4 vw[NC];
-  float sq = 0.f;
+  const bool rot = a.cos != nullptr;
+  // every load of the row is issued before the first reduction
+  uint4 kw[NC], vw[NC], ww[NC];
+  float4 cs[NC], sn[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int ch = lane + LPR * c;
-    rows::unpack8(ch < n_chunks ? rows::ld16(krow + ch * 8) : make_uint4(0, 0, 0, 0), x[c]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sq += x[c][i] * x[c][i];
+    const bool valid = ch < n_chunks;
+    kw[c] = valid ? rows::ld16(krow + ch * 8) : make_uint4(0, 0, 0, 0);
+    ww[c] = valid ? rows::ld16(a.w + ch * 8) : make_uint4(0, 0, 0, 0);
+    const int64_t p0 = static_cast<int64_t>(t) * (kHeadDim / 2) + (ch & 15) * 4;  // first pair of the chunk
+    cs[c] = valid && rot ? *reinterpret_cast<const float4*>(a.cos + p0) : make_float4(1.f, 1.f, 1.f, 1.f);
+    sn[c] = valid && rot ? *reinterpret_cast<const float4*>(a.sin + p0) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (a.v) {
     const uint16_t* vrow = a.v + static_cast<int64_t>(t) * a.ld_kv;
@@ -302,28 +311,31 @@ __global__ __launch_bounds__(256) void k_norm_rope_pack_kernel(KNormPackArgs a) 
   }
   int64_t code_row0 = 0, scale0 = 0;
   const bool placed = token_slot(a.geom, static_cast<uint32_t>(t), code_row0, scale0);
+  float sq = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float x[8];
+    rows::unpack8(kw[c], x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sq += x[i] * x[i];
+  }
   const float ms = rows::row_sum<LPR>(sq, red) / static_cast<float>(n_chunks * 8);
   const float rn = 1.0f / sqrtf(ms + a.eps);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int ch = lane + LPR * c;
     const bool valid = ch < n_chunks;
-    float wv[8];
-    rows::unpack8(valid ? rows::ld16(a.w + ch * 8) : make_uint4(0, 0, 0, 0), wv);
-    float y[8];
+    float x[8], wv[8], y[8];
+    rows::unpack8(kw[c], x);
+    rows::unpack8(ww[c], wv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = x[c][i] * rn;
+    for (int i = 0; i < 8; ++i) y[i] = x[i] * rn;
     rows::rbf8(y);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = y[i] * wv[i];
     rows::rbf8(y);
     if (a.ku && valid) rows::st16(a.ku + static_cast<int64_t>(t) * a.ld_ku + ch * 8, rows::pack8(y));
-    if (a.cos) {
-      const int64_t p0 = static_cast<int64_t>(t) * (kHeadDim / 2) + (ch & 15) * 4;  // first pair of the chunk
-      const float4 c4 = valid ? *reinterpret_cast<const float4*>(a.cos + p0) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 s4 = valid ? *reinterpret_cast<const float4*>(a.sin + p0) : make_float4(0.f, 0.f, 0.f, 0.f);
-      rope4_bf16(y, c4, s4);
-    }
+    if (rot) rope4_bf16(y, cs[c], sn[c]);
     pack_head_chunk(y, ch, valid, placed, a.geom, code_row0, scale0, a.kpool);
   }
   if (a.v) {
@@ -512,7 +524,8 @@ int wf_k_norm_rope_kv_pack(const void* k, const void* v, int64_t n_tokens, int32
   a.geom = wf::make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
   a.kpool = wf::PoolView{k_codes, k_scales};
   a.vpool = wf::PoolView{v_codes, v_scales};
-  const uint32_t grid = static_cast<uint32_t>((n_tokens + 256 / lpr - 1) / (256 / lpr));
+  const uint32_t n_blk = static_cast<uint32_t>((n_tokens + 256 / lpr - 1) / (256 / lpr));
+  const uint32_t grid = (n_blk + wf::kNumXcd - 1) / wf::kNumXcd * wf::kNumXcd;
   wf::rows::dispatch_shape(lpr, nc, [&](auto L, auto C) {
     hipLaunchKernelGGL((wf::k_norm_rope_pack_kernel<decltype(L)::value, decltype(C)::value>), dim3(grid), dim3(256),
                        0, wf::as_stream(stream), a);
