@@ -51,46 +51,63 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
   const int f = t / a.frame_tokens;
   uint16_t* row = a.x + static_cast<int64_t>(t) * a.ldx;
 
-  uint4 xr[NC], yr[NC], gr[NC];
+  // The row is kept as packed bf16 (4 registers per chunk) and unpacked in
+  // each pass; the affine and modulation rows are fetched with the row, so
+  // every load is in flight before the first reduction.
+  const bool mod = a.shift || a.scale;
+  uint4 xr[NC], pa[NC], pb[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int ch = lane + LPR * c;
     const bool ok = ch < n_chunks;
-    xr[c] = ok ? ld16(row + ch * 8) : make_uint4(0, 0, 0, 0);
-    if (a.ry) yr[c] = ok ? ld16(a.ry + static_cast<int64_t>(t) * a.ldry + ch * 8) : make_uint4(0, 0, 0, 0);
-    if (a.rgate) gr[c] = ok ? ld16(a.rgate + static_cast<int64_t>(f) * a.ld_rgate + ch * 8) : make_uint4(0, 0, 0, 0);
-  }
-  float v[NC][8];
-  float sum = 0.f;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    unpack8(xr[c], v[c]);
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    xr[c] = ok ? ld16(row + ch * 8) : z;
     if (a.ry) {
-      float y[8];
-      unpack8(yr[c], y);
+      uint4 yr = ok ? ld16(a.ry + static_cast<int64_t>(t) * a.ldry + ch * 8) : z;
+      uint4 gr = a.rgate && ok ? ld16(a.rgate + static_cast<int64_t>(f) * a.ld_rgate + ch * 8) : z;
+      // residual, applied as soon as its operands arrive
+      float v[8], y[8];
+      unpack8(xr[c], v);
+      unpack8(yr, y);
       if (a.rgate) {
         float g[8];
-        unpack8(gr[c], g);
+        unpack8(gr, g);
 #pragma unroll
         for (int i = 0; i < 8; ++i) y[i] = y[i] * g[i];
         rbf8(y);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + y[i];
-      rbf8(v[c]);
-      if (lane + LPR * c < n_chunks) st16(row + (lane + LPR * c) * 8, pack8(v[c]));
+      for (int i = 0; i < 8; ++i) v[i] = v[i] + y[i];
+      xr[c] = pack8(v);
+      if (ok) st16(row + ch * 8, xr[c]);
     }
+    // pa/pb: (shift, scale) of the modulation if there is one, else the affine (w, b)
+    if (mod) {
+      if (a.shift) pa[c] = ok ? ld16(a.shift + static_cast<int64_t>(f) * a.ld_mod + ch * 8) : z;
+      if (a.scale) pb[c] = ok ? ld16(a.scale + static_cast<int64_t>(f) * a.ld_mod + ch * 8) : z;
+    } else {
+      if (a.w) pa[c] = ok ? ld16(a.w + ch * 8) : z;
+      if (a.b) pb[c] = ok ? ld16(a.b + ch * 8) : z;
+    }
+  }
+  float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sum += v[c][i];
+  for (int c = 0; c < NC; ++c) {
+    float v[8];
+    unpack8(xr[c], v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum += v[i];
   }
   const float mean = row_sum<LPR>(sum, red[0]) / static_cast<float>(a.dim);
   float sq = 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     if (lane + LPR * c < n_chunks) {
+      float v[8];
+      unpack8(xr[c], v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float d = v[c][i] - mean;
+        const float d = v[i] - mean;
         sq += d * d;
       }
     }
@@ -102,20 +119,26 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
   for (int c = 0; c < NC; ++c) {
     const int ch = lane + LPR * c;
     if (ch < n_chunks) {
-      float wv[8], bv[8], sh[8], sc[8];
-      if (a.w) unpack8(ld16(a.w + ch * 8), wv);
-      if (a.b) unpack8(ld16(a.b + ch * 8), bv);
-      if (a.shift) unpack8(ld16(a.shift + static_cast<int64_t>(f) * a.ld_mod + ch * 8), sh);
-      if (a.scale) unpack8(ld16(a.scale + static_cast<int64_t>(f) * a.ld_mod + ch * 8), sc);
-      float y[8];
+      float v[8], y[8];
+      unpack8(xr[c], v);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        y[i] = (v[c][i] - mean) * rstd;
-        if (a.w) y[i] = y[i] * wv[i];
-        if (a.b) y[i] = y[i] + bv[i];
+      for (int i = 0; i < 8; ++i) y[i] = (v[i] - mean) * rstd;
+      if (a.w) {
+        float wv[8];
+        unpack8(mod ? ld16(a.w + ch * 8) : pa[c], wv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = y[i] * wv[i];
+      }
+      if (a.b) {
+        float bv[8];
+        unpack8(mod ? ld16(a.b + ch * 8) : pb[c], bv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = y[i] + bv[i];
       }
       rbf8(y);
       if (a.scale) {
+        float sc[8];
+        unpack8(pb[c], sc);
 #pragma unroll
         for (int i = 0; i < 8; ++i) sc[i] = 1.0f + sc[i];
         rbf8(sc);
@@ -124,16 +147,16 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
         rbf8(y);
       }
       if (a.shift) {
+        float sh[8];
+        unpack8(pa[c], sh);
 #pragma unroll
         for (int i = 0; i < 8; ++i) y[i] = y[i] + sh[i];
         rbf8(y);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        v[c][i] = y[i];
-        amax = fmaxf(amax, fabsf(y[i]));
-      }
-      if (a.out) st16(a.out + static_cast<int64_t>(t) * a.ldo + ch * 8, pack8(v[c]));
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(y[i]));
+      xr[c] = pack8(y);
+      if (a.out) st16(a.out + static_cast<int64_t>(t) * a.ldo + ch * 8, xr[c]);
     }
   }
   if (a.q) {
@@ -145,7 +168,11 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int ch = lane + LPR * c;
-      if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8_i8(v[c], s, r);
+      if (ch < n_chunks) {
+        float y[8];
+        unpack8(xr[c], y);
+        *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8_i8(y, s, r);
+      }
     }
   }
 }
