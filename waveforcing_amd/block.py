@@ -181,6 +181,32 @@ class QuantizedWanBlock:
         self.cnorm_k = params.cnorm_k.to(dev)
         self._ws: dict = {}
 
+    @classmethod
+    def from_packed(cls, packed: dict, heads: int, device="cuda") -> "QuantizedWanBlock":
+        """A block from offline-packed tensors (waveforcing_amd.checkpoint.pack_block /
+        load_packed): int8 weights and scales go to the GPU as they are, nothing is quantized."""
+        self = cls.__new__(cls)
+        dev = self.device = torch.device(device)
+
+        def lin(name):
+            b = packed.get(f"{name}_b")
+            return QLinear(packed[f"{name}_i8"].to(dev).contiguous(), packed[f"{name}_scale"].to(dev).contiguous(),
+                           None if b is None else b.to(dev).contiguous())
+
+        q, k, v = lin("q"), lin("k"), lin("v")
+        self.qkv = QLinear(torch.cat([q.w, k.w, v.w], 0), torch.cat([q.s, k.s, v.s], 0),
+                           torch.cat([q.b, k.b, v.b], 0))
+        self.o, self.cq, self.ck, self.cv, self.co = lin("o"), lin("cq"), lin("ck"), lin("cv"), lin("co")
+        self.fc_in, self.fc_out = lin("fc_in"), lin("fc_out")
+        self.dim = self.qkv.w.shape[1]
+        self.heads = heads
+        self.head_dim = self.dim // heads
+        self.ffn_dim = self.fc_in.w.shape[0]
+        for name in ("modulation", "norm_q", "norm_k", "norm3_w", "norm3_b", "cnorm_q", "cnorm_k"):
+            setattr(self, name, packed[name].to(dev).contiguous())
+        self._ws = {}
+        return self
+
     # -- workspace (allocated once per token count; the kernels never allocate)
     def _workspace(self, T: int) -> dict:
         ws = self._ws.get(T)
