@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
   if (a.q) {
     amax = row_max_nonneg<LPR>(amax, red[2]);
     const float s = i8_scale(amax);
-    const float r = __frcp_rn(s);
+    const double rd = i8_recip(s);
     if (lane == 0) a.qs[t] = s;
     int8_t* qrow = a.q + static_cast<int64_t>(t) * a.dim;
 #pragma unroll
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
       if (ch < n_chunks) {
         float y[8];
         unpack8(xr[c], y);
-        *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8_i8(y, s, r);
+        *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8_i8(y, rd);
       }
     }
   }

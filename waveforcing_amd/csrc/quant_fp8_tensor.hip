@@ -4,7 +4,7 @@
 //     s = max(amax|w| / 448, 1e-8);  code = e4m3(fp32(w) / s)
 //   activations (fp8.py:47-48), bf16 tensor arithmetic:
 //     s = max(bf16(amax|x| / 448), bf16(1e-8));  code = e4m3(bf16(x / s))
-// Divisions are IEEE (correctly rounded), as torch's are.  The quotient's
+// Quotients are the IEEE (correctly rounded) fp32 ones, as torch's are.  The quotient's
 // magnitude is at most 448 (weights: 448 * (1 + 2^-23); activations, with s
 // rounded to bf16: 450 after the bf16 rounding), where e4m3's round-to-
 // nearest-even gives 448 (values up to 464 round there); clamping to 448 and
@@ -75,6 +75,11 @@ __global__ __launch_bounds__(kThreads) void quant_tensor_kernel(Geometry g, cons
     s = fmaxf(__fdiv_rn(amax, kE4M3Max), 1e-8f);
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
+  // RN32(x / s) as RN32(RN64(x * RN64(1 / s))): equal to the IEEE fp32
+  // quotient for all fp32 x, s (an fp32 quotient is never an fp32 rounding
+  // midpoint and otherwise lies >= 2^-49 relative from one; the fp64 product
+  // is within 2^-52), at fp64-multiply cost instead of a division sequence.
+  const double rd = 1.0 / static_cast<double>(s);
   for (int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; c < g.total;
        c += static_cast<int64_t>(gridDim.x) * kThreads) {
     const uint4 w = *reinterpret_cast<const uint4*>(chunk_ptr(g, c));
@@ -82,8 +87,8 @@ __global__ __launch_bounds__(kThreads) void quant_tensor_kernel(Geometry g, cons
     float q[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      q[2 * i] = __fdiv_rn(bf16_lo_to_f32(u[i]), s);
-      q[2 * i + 1] = __fdiv_rn(bf16_hi_to_f32(u[i]), s);
+      q[2 * i] = static_cast<float>(static_cast<double>(bf16_lo_to_f32(u[i])) * rd);
+      q[2 * i + 1] = static_cast<float>(static_cast<double>(bf16_hi_to_f32(u[i])) * rd);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {

@@ -8,11 +8,9 @@
 // wave_rt/runtime/fp8.py:33-35,47-48; this is its per-token / per-channel
 // int8 counterpart with the same clamp(min=1e-8) floor).
 //
-// x / s is formed as q = |x| * r, r = RN(1/s), refined once with the exact
-// residual fma(-q, s, |x|); a 1-ulp error of that quotient can only change
-// the integer rounding when the quotient sits within one ulp of k + 1/2, and
-// those elements are recomputed with a full IEEE division, so the result is
-// round_half_even(RN(x / s)) exactly.
+// x / s is formed as RN32(RN64(x * RN64(1/s))), which equals the IEEE fp32
+// quotient for every fp32 x and s (rows::quant_i8 gives the argument), then
+// rounded half to even, so the result is round_half_even(RN(x / s)) exactly.
 //
 // Rows up to 16384 wide run on the row engine of rows.hpp (one wave per row
 // up to 2048, one workgroup per row above; the row stays in registers
@@ -34,19 +32,6 @@ __device__ inline float wave_max(float v) {
   return v;
 }
 
-__device__ inline int8_t quant_one(float x, float s, float r) {
-  const float ax = fabsf(x);
-  float q = ax * r;
-  q = fmaf(fmaf(-q, s, ax), r, q);
-  const float k = rintf(q);
-  const float d = fabsf(q - k);
-  // 1 ulp of q for q < 2^24 is at most q * 2^-23.
-  if (fabsf(d - 0.5f) <= q * 1.1920929e-7f) q = __fdiv_rn(ax, s);
-  float qi = fminf(rintf(q), 127.0f);
-  qi = x < 0.f ? -qi : qi;
-  return static_cast<int8_t>(static_cast<int>(qi));
-}
-
 __device__ inline float amax8(const uint4& a) {
   const uint32_t w[4] = {a.x, a.y, a.z, a.w};
   float m = 0.f;
@@ -55,21 +40,11 @@ __device__ inline float amax8(const uint4& a) {
   return m;
 }
 
-__device__ inline uint2 quant8(const uint4& a, float s, float r) {
-  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-  uint32_t packed[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int8_t q0 = quant_one(bf16_lo_to_f32(w[2 * i]), s, r);
-    const int8_t q1 = quant_one(bf16_hi_to_f32(w[2 * i]), s, r);
-    const int8_t q2 = quant_one(bf16_lo_to_f32(w[2 * i + 1]), s, r);
-    const int8_t q3 = quant_one(bf16_hi_to_f32(w[2 * i + 1]), s, r);
-    packed[i] = (static_cast<uint32_t>(static_cast<uint8_t>(q0))) |
-                (static_cast<uint32_t>(static_cast<uint8_t>(q1)) << 8) |
-                (static_cast<uint32_t>(static_cast<uint8_t>(q2)) << 16) |
-                (static_cast<uint32_t>(static_cast<uint8_t>(q3)) << 24);
-  }
-  return make_uint2(packed[0], packed[1]);
+// 8 bf16 values -> 8 int8 codes (rows::quant8_i8 with rd = RN64(1/s)).
+__device__ inline uint2 quant8(const uint4& a, double rd) {
+  float v[8];
+  rows::unpack8(a, v);
+  return rows::quant8_i8(v, rd);
 }
 
 // K % 8 == 0 (checked at the entry point): every 8-element chunk is whole.
@@ -95,15 +70,15 @@ __global__ __launch_bounds__(kThreads) void quant_rows_i8_kernel(const uint16_t*
     amax = fmaxf(amax, amax8(*reinterpret_cast<const uint4*>(row + ch * 8)));
   amax = wave_max(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-8f);
-  const float r = __frcp_rn(s);
+  const double rd = rows::i8_recip(s);
   if (lane == 0) scales[m] = s;
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
     const int64_t ch = lane + 64 * c;
-    if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(reg[c], s, r);
+    if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(reg[c], rd);
   }
   for (int64_t ch = lane + 64 * kRegChunks; ch < n_chunks; ch += 64)
-    *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(*reinterpret_cast<const uint4*>(row + ch * 8), s, r);
+    *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(*reinterpret_cast<const uint4*>(row + ch * 8), rd);
 }
 
 // Row-engine variant: LPR lanes per row, NC chunks of 8 per lane.
@@ -129,13 +104,13 @@ __global__ __launch_bounds__(256) void quant_rows_i8_row_kernel(const uint16_t* 
   for (int c = 0; c < NC; ++c) amax = fmaxf(amax, amax8(reg[c]));
   amax = rows::row_max_nonneg<LPR>(amax, red);
   const float s = rows::i8_scale(amax);
-  const float r = __frcp_rn(s);
+  const double rd = rows::i8_recip(s);
   if (lane == 0) scales[m] = s;
   int8_t* qrow = q + static_cast<int64_t>(m) * ldq;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int ch = lane + LPR * c;
-    if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(reg[c], s, r);
+    if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(reg[c], rd);
   }
 }
 

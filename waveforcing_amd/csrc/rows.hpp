@@ -116,25 +116,25 @@ __device__ inline uint4 pack8(const float* f) {
 __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ inline void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
 
-// int8 code of x with scale s (reciprocal r = RN(1/s)): round_half_even(RN(x / s))
-// clamped to +-127.  q = |x| r refined by one exact residual step is within
-// one ulp of RN(|x| / s); only a quotient within one ulp of k + 1/2 can round
-// differently, and those are recomputed by IEEE division.
-__device__ inline int quant_i8(float x, float s, float r) {
-  const float ax = fabsf(x);
-  float q = ax * r;
-  q = fmaf(fmaf(-q, s, ax), r, q);
-  const float k = rintf(q);
-  if (fabsf(fabsf(q - k) - 0.5f) <= q * 1.1920929e-7f) q = __fdiv_rn(ax, s);
-  const float qi = fminf(rintf(q), 127.0f);
-  return static_cast<int>(x < 0.f ? -qi : qi);
+// int8 code of x with scale s: round_half_even(RN32(x / s)) clamped to
+// +-127, given rd = RN64(1 / s) (i8_recip).  RN32(x / s) is computed as
+// RN32(RN64(x * rd)): the fp64 product is within 2^-52 (relative) of x / s,
+// while the quotient of two fp32 values is never an fp32 rounding midpoint
+// (a 25-bit odd significand times a 24-bit one needs more than 24 bits) and
+// otherwise lies at least 2^-49 (relative) away from every midpoint, so the
+// fp32 rounding of the product is that of the IEEE quotient.  gfx950 runs
+// fp64 multiplies and conversions at the rate of its unpacked fp32 ones.
+__device__ inline double i8_recip(float s) { return 1.0 / static_cast<double>(s); }
+__device__ inline int quant_i8(float x, double rd) {
+  const float q = static_cast<float>(static_cast<double>(x) * rd);
+  return static_cast<int>(fminf(fmaxf(rintf(q), -127.0f), 127.0f));
 }
-__device__ inline uint2 quant8_i8(const float* v, float s, float r) {
+__device__ inline uint2 quant8_i8(const float* v, double rd) {
   uint32_t lo = 0, hi = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lo |= (static_cast<uint32_t>(quant_i8(v[i], s, r)) & 0xffu) << (8 * i);
+  for (int i = 0; i < 4; ++i) lo |= (static_cast<uint32_t>(quant_i8(v[i], rd)) & 0xffu) << (8 * i);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) hi |= (static_cast<uint32_t>(quant_i8(v[4 + i], s, r)) & 0xffu) << (8 * i);
+  for (int i = 0; i < 4; ++i) hi |= (static_cast<uint32_t>(quant_i8(v[4 + i], rd)) & 0xffu) << (8 * i);
   return make_uint2(lo, hi);
 }
 // Per-token int8 scale: max(amax / 127, 1e-8) in fp32.
