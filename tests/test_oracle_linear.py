@@ -99,3 +99,29 @@ def test_fp8_scaled_mm_matches_decoded_product():
     x_fp8, a_scale = olin.fp8_quant_act(x)
     ref = (x_fp8.double() @ w_fp8.double().t()) * float(a_scale) * float(w_scale) + b.double()
     assert torch.allclose(y.double(), ref, rtol=2 ** -7, atol=1e-4)
+
+
+def test_fp32_quotient_equals_rounded_fp64_reciprocal_product():
+    """The quantizers form x / s as RN32(RN64(x * RN64(1 / s))); for fp32 x and s this is the IEEE fp32
+    quotient the oracle's torch division gives, also next to exact halfway points of the integer rounding."""
+    rng = np.random.default_rng(7)
+    n = 2_000_000
+    amax = (rng.random(n, dtype=np.float32) * 100 + 1e-3).astype(np.float32)
+    x = (rng.standard_normal(n).astype(np.float32) * amax / 3).astype(np.float32)
+    x = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)           # bf16 activations
+    s = np.maximum(amax / np.float32(127), np.float32(1e-8)).astype(np.float32)
+    cases = [(x, s)]
+    k = rng.integers(-127, 127, n).astype(np.float32)
+    s2 = (rng.random(n, dtype=np.float32) * 3 + 0.01).astype(np.float32)
+    mid = ((k + np.float32(0.5)) * s2).astype(np.float32)
+    for d in (-2, -1, 0, 1, 2):                                      # neighbours of k + 1/2 quotients
+        cases.append(((mid.view(np.int32) + d).view(np.float32), s2))
+    e4 = (rng.integers(-448, 449, n) / 8).astype(np.float32)        # e4m3-range quotients
+    cases.append(((e4 * s2).astype(np.float32), s2))
+    for xs, ss in cases:
+        ref = (xs / ss).astype(np.float32)
+        got = (xs.astype(np.float64) * (1.0 / ss.astype(np.float64))).astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # a plain fp32 reciprocal product is not enough (so the check has teeth)
+    xs, ss = cases[3]
+    assert not np.array_equal((xs * (np.float32(1) / ss)).astype(np.float32), (xs / ss).astype(np.float32))
