@@ -1,8 +1,8 @@
 """The Wan attention block on the quantized HIP path, for one chunk on one GPU.
 
 Restates CausalWanAttentionBlock.forward
-(naive_rt/rolling_forcing/wan/modules/causal_model.py:349-402), the block that
-WaveRT's SGLang model runs (F4 of the path's survey), with:
+(naive_rt/rolling_forcing/wan/modules/causal_model.py:349-402), the naive_rt
+counterpart of the block WaveRT's SGLang model runs (SGLang is not vendored), with:
 
 * every block linear W8A8 int8 (the ``scope=all`` swap of
   wave_rt/runtime/fp8.py:93-137, per-token / per-channel int8);
