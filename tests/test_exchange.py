@@ -55,3 +55,19 @@ def test_slots_run_out_loudly():
         x.reserve(0)
     with pytest.raises(RuntimeError, match="no free slot"):
         x.reserve(0)
+
+
+def test_denoise_step_must_release_its_slots_before_the_next():
+    x = ex.PagedExchange(n_layers=1, n_heads=1, tokens_per_frame=16, device="cpu")
+    x.make_denoise_exch(0)
+    x._denoise_slots[0] = x.reserve(0)   # as the closure does on its first call
+    with pytest.raises(RuntimeError, match="finish_denoise"):
+        x.make_denoise_exch(3)
+    x.finish_denoise()
+    x.make_denoise_exch(3)
+
+
+def test_anchor_promotion_needs_the_unrotated_key():
+    x = ex.PagedExchange(n_layers=1, n_heads=1, tokens_per_frame=16, device="cpu")
+    with pytest.raises(RuntimeError, match="unroped_key"):
+        x.promote({0: (x.reserve(0), None)}, cid=0)

@@ -98,6 +98,8 @@ class PagedExchange:
         key = (layer, tuple(slots))
         t = self._tables.get(key)
         if t is None:
+            if len(self._tables) >= 4096:  # slot tuples recur as the ring turns; bound the cache anyway
+                self._tables.clear()
             pages = [p for s in slots for p in self.slot_pages(s)]
             t = self.pools[layer].page_table(pages)
             self._tables[key] = t
@@ -162,6 +164,8 @@ class PagedExchange:
         :meth:`finish_denoise` releases them after the forward.
         """
         qf = self.npb if query_frames is None else query_frames
+        if getattr(self, "_denoise_slots", None):
+            raise RuntimeError("[paged] the previous denoise step still holds slots; call finish_denoise() first")
         self._denoise_slots: dict[int, int] = {}
 
         def exch(*, layer_idx, roped_query, roped_key, unroped_key, value, current_start=None,
@@ -215,6 +219,8 @@ class PagedExchange:
         for L, (slot, ku) in sorted(store_kv.items()):
             keep = None
             if not self.clean[L]:
+                if ku is None:
+                    raise RuntimeError(f"[paged] layer {L}: the anchor chunk needs its unroped_key")
                 k = ku[0] if ku.dim() == 4 else ku
                 keep = k.contiguous().clone()
             self.append_clean(L, CleanPage(cid=cid, slot=slot, ku=keep))

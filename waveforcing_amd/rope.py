@@ -17,6 +17,7 @@ from __future__ import annotations
 import torch
 
 _CACHE: dict = {}
+_CACHE_MAX = 64
 
 
 def split_pairs(head_dim: int) -> tuple[int, int, int]:
@@ -48,6 +49,9 @@ def cos_sin(frames: int, height: int, width: int, start_frame: int = 0, head_dim
     key = (frames, height, width, start_frame, head_dim, str(device))
     hit = _CACHE.get(key)
     if hit is None:
+        # the anchor's start frame moves every step of a long stream: keep the cache bounded
+        if len(_CACHE) >= _CACHE_MAX:
+            _CACHE.pop(next(iter(_CACHE)))
         a = angles(frames, height, width, start_frame, head_dim)
         hit = (torch.cos(a).float().contiguous().to(device), torch.sin(a).float().contiguous().to(device))
         _CACHE[key] = hit
