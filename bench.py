@@ -328,6 +328,57 @@ def cpu_baseline_kv() -> dict:
     }
 
 
+def _cpu_median(fn, reps: int = 5, budget_s: float = 6.0) -> float:
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 2 or (len(times) < reps and time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_baseline_extra() -> dict:
+    """The oracle's torch-CPU path of the other workloads, timed on this host: the int8 W8A8 linear at the
+    1.3B shape (whole), the reference's per-tensor e4m3 linear (64 rows) and the attention over 8 chunks
+    (256 queries of one head against all 37440 keys), the last two extrapolated to the full workload."""
+    from oracle import attention as oat
+    from oracle import linear as olin
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    out = {}
+    x, w, b = inputs.linear_1p3b()
+    ops = 2.0 * x.shape[0] * w.shape[0] * x.shape[1]
+    t = _cpu_median(lambda: olin.i8_linear(x, w, b))
+    out["w8a8_int8_linear"] = {"value": round(ops / t / 1e12, 4), "unit": "TOPS", "ms": round(t * 1e3, 2),
+                               "cores": threads, "kind": "port",
+                               "sample": "oracle int8 linear 4680x1536x1536 incl. quantization (torch _int_mm)"}
+    wq, ws = olin.fp8_quant_weight(w)
+    rows = 64  # torch's CPU _scaled_mm is slow (~80 s for the whole 4680-row linear): a bounded sample
+    t = _cpu_median(lambda: olin.fp8_linear(x[:rows], wq, ws, b), reps=3)
+    ops_s = 2.0 * rows * w.shape[0] * x.shape[1]
+    out["fp8_pertensor_linear"] = {"value": round(ops_s / t / 1e12, 6), "unit": "TFLOP/s",
+                                   "ms_full_workload_extrapolated": round(t * x.shape[0] / rows * 1e3, 1),
+                                   "cores": threads, "kind": "port",
+                                   "sample": "oracle per-tensor e4m3 linear, 64 of the 4680 rows x 1536 x 1536 "
+                                             "(torch _scaled_mm)"}
+    g = torch.Generator().manual_seed(12)
+    n_kv, lq = 8 * TOKENS, 256
+    q = torch.randn((lq, 1, HEAD_DIM), generator=g).to(torch.bfloat16)
+    kv = torch.randn((n_kv, 1, HEAD_DIM), generator=g).to(torch.bfloat16)
+    t = _cpu_median(lambda: oat.sdpa(q, kv, kv), reps=3)
+    flops = 4.0 * lq * n_kv * HEAD_DIM
+    full_ms = t * (TOKENS * HEADS) / lq * 1e3
+    out["attention_8_chunks"] = {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s",
+                                 "ms_full_workload_extrapolated": round(full_ms, 1), "cores": threads, "kind": "port",
+                                 "sample": "oracle SDPA, 256 queries x 1 head over 37440 keys, fp32; x 219.4 "
+                                           "extrapolates to 4680 queries x 12 heads"}
+    return out
+
+
 def main() -> None:
     global WARM_SECONDS
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -337,7 +388,7 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
                     help="minimum untimed warm-up of the KV workloads (profiler runs use 0)")
-    ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention",
+    ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
@@ -355,7 +406,8 @@ def main() -> None:
               "kv_unpack": lambda s, w, d: bench_kv(s, w, d, ("unpack",)), "gemm": bench_gemm,
               "linears_1p3b": bench_block_linears, "attention": bench_attention, "copy": bench_copy,
               "block_1p3b": lambda s, w, d: bench_block("1.3b", s, w, d),
-              "block_14b": lambda s, w, d: bench_block("14b", s, w, d), "exchange_1p3b": bench_exchange}[args.only]
+              "block_14b": lambda s, w, d: bench_block("14b", s, w, d), "exchange_1p3b": bench_exchange,
+              "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
     kv = bench_kv(args.steps, args.warmup, dev)
@@ -367,6 +419,7 @@ def main() -> None:
     b14 = bench_block("14b", max(3, args.steps // 10), 1, dev)
     xch = bench_exchange(max(5, args.steps // 5), 2, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
+    cpu_extra = None if args.no_cpu_baseline else cpu_baseline_extra()
     # one launch per step: the launch duration is the step time
     achieved = kv["bytes_per_step"] / (kv["ms_pack"] * 1e-3) / 1e9
     line = {
@@ -396,6 +449,7 @@ def main() -> None:
             "traffic": profiled_traffic("fp8_kv_pack_30_layers"),
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_extra": cpu_extra,
         "extra": {
             "fp8_kv_unpack_gbs": round(kv["unpack_gbs"], 2),
             "fp8_kv_unpack_frac": round(kv["unpack_gbs"] / HBM_PEAK_GBS, 4),
