@@ -260,7 +260,8 @@ int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads,
 /* y = LayerNorm(x) (fp32 statistics, optional bf16 affine w/b, rounded to
  * bf16), then, if given, the bf16 modulation y = bf16(bf16(y * bf16(1 +
  * scale[f])) + shift[f]) with f = row / frame_tokens (scale/shift bf16
- * frame rows of stride ld_mod elements); writes y (bf16, row stride ldo) if
+ * frame rows of stride ld_mod elements, at least ceil(T / frame_tokens)
+ * of them: the kernel cannot check); writes y (bf16, row stride ldo) if
  * out != NULL and its per-token int8 quantization (as wf_act_quant_i8) if
  * q != NULL.  dim % 8 == 0, dim <= 16384.  Replaces norm1/norm2 +
  * modulation (naive_rt/rolling_forcing/wan/modules/causal_model.py:381,
@@ -273,7 +274,8 @@ int wf_ln_modulate_quant(const void* x, int64_t T, int32_t dim, int64_t ldx,
                          void* stream);
 
 /* The residual that precedes a norm, fused into it: first, in place,
- * x = bf16(x + bf16(y * gate[f])) (gate frame rows of stride ld_gate), or
+ * x = bf16(x + bf16(y * gate[f])) (gate frame rows of stride ld_gate,
+ * at least ceil(T / frame_tokens) of them), or
  * x = bf16(x + y) when gate is NULL, then wf_ln_modulate_quant of the
  * updated x (out must not alias x).  y == NULL skips the residual.  The
  * self-attention residual + norm3 (causal_model.py:386-390) and the
@@ -297,9 +299,9 @@ int wf_rmsnorm_rope(const void* x, int64_t T, int32_t dim, int64_t ldx,
                     int64_t ldo, void* stream);
 
 /* In place x = bf16(x + bf16(y * gate[row / frame_tokens])), or
- * x = bf16(x + y) when gate is NULL (gate bf16 frame rows of stride
- * ld_gate elements).  The gated residuals of causal_model.py:386,397-398
- * and the cross-attention residual of :390. */
+ * x = bf16(x + y) when gate is NULL (ceil(T / frame_tokens) gate bf16
+ * frame rows of stride ld_gate elements).  The gated residuals of
+ * causal_model.py:386,397-398 and the cross-attention residual of :390. */
 int wf_gate_residual(void* x, int64_t ldx, const void* y, int64_t ldy,
                      const void* gate, int64_t ld_gate, int64_t T,
                      int32_t dim, int32_t frame_tokens, void* stream);
