@@ -88,14 +88,16 @@ def rope_apply_table(x, cos, sin):
 
 
 def block_forward(p, x, e, grid, start_frame, pool_k, pool_v, context_table, own_table, n_context, page_tokens,
-                  text_k, text_v, heads):
+                  text_k, text_v, heads, return_unroped_k=False):
     """One block on the CPU.
 
     p: waveforcing_amd.block.BlockParams (CPU bf16); x [T, dim] bf16;
     e [F, 6, dim] bf16; grid = (frames, height, width) of the chunk;
     pool_k / pool_v: (codes, scales) CPU pools holding the prior context, into
     which this chunk's K/V are packed at own_table (modified in place);
-    text_k / text_v [L, H, D] bf16.  Returns the new x.
+    text_k / text_v [L, H, D] bf16.  Returns the new x, and with
+    ``return_unroped_k`` also the chunk's normalized, un-rotated K [T, H, D]
+    (the exchange's unroped_key).
     """
     T, dim = x.shape
     frames, height, width = grid
@@ -113,11 +115,11 @@ def block_forward(p, x, e, grid, start_frame, pool_k, pool_v, context_table, own
     a = layer_norm(x)
     a = a * (1 + per_frame(a, 1)) + per_frame(a, 0)
     q = rms_norm(lin(a, p.q_w, p.q_b), p.norm_q).view(T, heads, hd)
-    k = rms_norm(lin(a, p.k_w, p.k_b), p.norm_k).view(T, heads, hd)
+    ku = rms_norm(lin(a, p.k_w, p.k_b), p.norm_k).view(T, heads, hd)
     v = lin(a, p.v_w, p.v_b).view(T, heads, hd)
     ang = rope_angles(frames, height, width, start_frame, hd)
     q = rope_apply(q, ang)
-    k = rope_apply(k, ang)
+    k = rope_apply(ku, ang)
     okv.pack(k, own_table, page_tokens, *pool_k)
     okv.pack(v, own_table, page_tokens, *pool_v)
     y = oat.paged_fp8(q, pool_k, pool_v, context_table, n_context, page_tokens).to(torch.bfloat16)
@@ -135,7 +137,8 @@ def block_forward(p, x, e, grid, start_frame, pool_k, pool_v, context_table, own
     h = h * (1 + per_frame(h, 4)) + per_frame(h, 3)
     f = lin(h, p.fc_in_w, p.fc_in_b, gelu=True)
     y = lin(f, p.fc_out_w, p.fc_out_b)
-    return x + y * per_frame(y, 5)
+    x = x + y * per_frame(y, 5)
+    return (x, ku) if return_unroped_k else x
 
 
 def text_kv(p, context, heads):

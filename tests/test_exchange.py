@@ -71,3 +71,26 @@ def test_anchor_promotion_needs_the_unrotated_key():
     x = ex.PagedExchange(n_layers=1, n_heads=1, tokens_per_frame=16, device="cpu")
     with pytest.raises(RuntimeError, match="unroped_key"):
         x.promote({0: (x.reserve(0), None)}, cid=0)
+
+
+def test_layer_context_holds_one_slot_per_layer_and_pass():
+    x = ex.PagedExchange(n_layers=2, n_heads=1, tokens_per_frame=16, device="cpu")
+    # store pass of the first chunk: no clean chunks yet, the context is the chunk itself
+    store_kv = {}
+    pool, ctx, own, n_ctx = x.layer_context(0, 0, 3, 4, 4, store_kv)
+    assert pool is x.pools[0] and n_ctx == x.T and len(own) == 3 and ctx.host == own.host
+    slot = store_kv[0][0]
+    assert own.host == x.slot_pages(slot)
+    # a second call of the same layer in the same pass reuses the slot
+    assert x.layer_context(0, 0, 3, 4, 4, store_kv)[2].host == own.host
+    x.layer_context(1, 0, 3, 4, 4, store_kv)
+    assert sorted(store_kv) == [0, 1] and len(x._free[0]) == x.n_slots - 1
+    x.abort_store(store_kv)
+    assert not store_kv and len(x._free[0]) == x.n_slots and len(x._free[1]) == x.n_slots
+    # denoise pass: slots held until finish_denoise
+    a = x.layer_context(0, 3, 3, 4, 4)[2].host
+    assert x.layer_context(0, 3, 3, 4, 4)[2].host == a and len(x._free[0]) == x.n_slots - 1
+    with pytest.raises(RuntimeError, match="finish_denoise"):
+        x.make_denoise_exch(3)
+    x.finish_denoise()
+    assert len(x._free[0]) == x.n_slots

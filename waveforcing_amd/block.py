@@ -79,19 +79,20 @@ class BlockParams:
         return BlockParams(**{f.name: getattr(self, f.name).to(device) for f in fields(self)})
 
 
-def random_block_params(dim: int, ffn_dim: int, seed: int = 0, w_std: float = 0.02) -> BlockParams:
-    """Seeded random-init block (CPU, bf16): linears ~ N(0, w_std), biases ~ N(0, 0.01), norm
-    weights ~ 1 + N(0, 0.05), modulation ~ N(0, 1) / sqrt(dim) (causal_model.py:347)."""
-    g = torch.Generator().manual_seed(seed)
+def random_block_params(dim: int, ffn_dim: int, seed: int = 0, w_std: float = 0.02, device="cpu") -> BlockParams:
+    """Seeded random-init block (bf16): linears ~ N(0, w_std), biases ~ N(0, 0.01), norm weights
+    ~ 1 + N(0, 0.05), modulation ~ N(0, 1) / sqrt(dim) (causal_model.py:347).  Drawn on ``device``
+    by that device's generator (the CPU and GPU draws of one seed differ)."""
+    g = torch.Generator(device=device).manual_seed(seed)
 
     def lin(o, i):
-        return (torch.randn((o, i), generator=g) * w_std).to(torch.bfloat16)
+        return (torch.randn((o, i), generator=g, device=device) * w_std).to(torch.bfloat16)
 
     def vec(n, std=0.01, mean=0.0):
-        return (torch.randn((n,), generator=g) * std + mean).to(torch.bfloat16)
+        return (torch.randn((n,), generator=g, device=device) * std + mean).to(torch.bfloat16)
 
     return BlockParams(
-        modulation=(torch.randn((1, 6, dim), generator=g) / dim ** 0.5).to(torch.bfloat16),
+        modulation=(torch.randn((1, 6, dim), generator=g, device=device) / dim ** 0.5).to(torch.bfloat16),
         q_w=lin(dim, dim), q_b=vec(dim), k_w=lin(dim, dim), k_b=vec(dim), v_w=lin(dim, dim), v_b=vec(dim),
         o_w=lin(dim, dim), o_b=vec(dim), norm_q=vec(dim, 0.05, 1.0), norm_k=vec(dim, 0.05, 1.0),
         norm3_w=vec(dim, 0.05, 1.0), norm3_b=vec(dim),

@@ -89,6 +89,7 @@ class PagedExchange:
         self.clean: list[list[CleanPage]] = [[] for _ in range(n_layers)]
         self._free: list[list[int]] = [list(range(self.n_slots)) for _ in range(n_layers)]
         self._tables: dict = {}
+        self._denoise_slots: dict[int, int] = {}  # layer -> slot of the chunk being denoised
 
     # ---------------------------------------------------------------- slots
     def slot_pages(self, slot: int) -> list[int]:
@@ -164,9 +165,8 @@ class PagedExchange:
         :meth:`finish_denoise` releases them after the forward.
         """
         qf = self.npb if query_frames is None else query_frames
-        if getattr(self, "_denoise_slots", None):
+        if self._denoise_slots:
             raise RuntimeError("[paged] the previous denoise step still holds slots; call finish_denoise() first")
-        self._denoise_slots: dict[int, int] = {}
 
         def exch(*, layer_idx, roped_query, roped_key, unroped_key, value, current_start=None,
                  tokens_per_frame=None, post_patch_height, post_patch_width, dim=None, rope_num_heads=None,
@@ -184,10 +184,36 @@ class PagedExchange:
 
         return exch
 
+    def layer_context(self, layer: int, chunk_start_frame: int, query_frames: int, height: int, width: int,
+                      store_kv: dict | None = None):
+        """(pool, context table, own table, context keys) of one layer for a block that packs its own
+        K/V (QuantizedWanBlock.forward): the chunk's slot is reserved (a denoise step's, released by
+        finish_denoise; or, with ``store_kv``, the stored chunk's, recorded for promote), the
+        anchor re-RoPEd, and the context is anchor + working set + the chunk."""
+        if store_kv is not None:
+            if layer not in store_kv:
+                store_kv[layer] = (self.reserve(layer), None)
+            slot = store_kv[layer][0]
+        else:
+            if layer not in self._denoise_slots:
+                self._denoise_slots[layer] = self.reserve(layer)
+            slot = self._denoise_slots[layer]
+        ctx_slots = self._anchor_working(layer, chunk_start_frame, query_frames, height, width)
+        if len(ctx_slots) + 1 > self.n_slots:
+            raise RuntimeError(f"[paged] active_slots={len(ctx_slots) + 1} > {self.n_slots}")
+        return (self.pools[layer], self.table(layer, ctx_slots + [slot]), self.table(layer, [slot]),
+                (len(ctx_slots) + 1) * self.T)
+
     def finish_denoise(self) -> None:
-        for L, slot in getattr(self, "_denoise_slots", {}).items():
+        for L, slot in self._denoise_slots.items():
             self.release(L, slot)
         self._denoise_slots = {}
+
+    def abort_store(self, store_kv: dict) -> None:
+        """Return the slots of a store pass that will not be promoted."""
+        for L, (slot, _) in store_kv.items():
+            self.release(L, slot)
+        store_kv.clear()
 
     def make_store_exch(self, chunk: int, store_kv: dict):
         """Store-side exchange (paged.py:257-310): the chunk's clean K/V go into a reserved slot that
@@ -222,6 +248,8 @@ class PagedExchange:
                 if ku is None:
                     raise RuntimeError(f"[paged] layer {L}: the anchor chunk needs its unroped_key")
                 k = ku[0] if ku.dim() == 4 else ku
+                if k.dim() == 2:  # [T, dim] rows of the block's K (QuantizedWanBlock unroped_k_out)
+                    k = k.view(k.shape[0], self.n_heads, self.head_dim)
                 keep = k.contiguous().clone()
             self.append_clean(L, CleanPage(cid=cid, slot=slot, ku=keep))
         store_kv.clear()
