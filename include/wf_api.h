@@ -306,6 +306,24 @@ int wf_gate_residual(void* x, int64_t ldx, const void* y, int64_t ldy,
                      const void* gate, int64_t ld_gate, int64_t T,
                      int32_t dim, int32_t frame_tokens, void* stream);
 
+/* ---------------------------------------------------------------------
+ * Re-noising for the next DMD step
+ * ------------------------------------------------------------------- */
+
+/* out = bf16((1 - sigma) * x0 + sigma * noise), every product, the
+ * difference 1 - sigma and the sum an fp32 operation: the
+ * FlowMatchScheduler.add_noise of _det_renoise
+ * (naive_rt/rolling_forcing/utils/scheduler.py:159-176,
+ * wave_rt/denoiser/engine.py:221-235) with one sigma for all frames.
+ * x0 and out are bf16 [batch][channels][frames][plane] (plane = h * w);
+ * noise is bf16 in the same layout, or frame-major
+ * [batch][frames][channels][plane] when noise_frame_major != 0 (the order
+ * _det_renoise draws it in).  out may alias x0, not a frame-major noise. */
+int wf_flow_add_noise_bf16(const void* x0, const void* noise, int64_t batch,
+                           int64_t channels, int64_t frames, int64_t plane,
+                           int32_t noise_frame_major, float sigma, void* out,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,7 @@ SIGNATURES: dict[str, list] = {
         _c_void_p,
     ],
     "wf_act_quant_i8": [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p],
+    "wf_flow_add_noise_bf16": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i32, _f32, _c_void_p, _c_void_p],
     "wf_gemm_i8": [
         _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
         _c_void_p, _i64, _c_void_p, _i32, _c_void_p,
