@@ -209,6 +209,12 @@ class QuantizedWanBlock:
         return self
 
     # -- workspace (allocated once per token count; the kernels never allocate)
+    def share_workspace(self, other: "QuantizedWanBlock") -> None:
+        """Use other's activation buffers (blocks of one shape that never run concurrently)."""
+        if (self.dim, self.ffn_dim, self.device) != (other.dim, other.ffn_dim, other.device):
+            raise ValueError("only blocks of the same shape and device can share a workspace")
+        self._ws = other._ws
+
     def _workspace(self, T: int) -> dict:
         ws = self._ws.get(T)
         if ws is None:

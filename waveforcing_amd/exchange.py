@@ -250,6 +250,6 @@ class PagedExchange:
                 k = ku[0] if ku.dim() == 4 else ku
                 if k.dim() == 2:  # [T, dim] rows of the block's K (QuantizedWanBlock unroped_k_out)
                     k = k.view(k.shape[0], self.n_heads, self.head_dim)
-                keep = k.contiguous().clone()
+                keep = k.contiguous().clone()   # the caller may reuse its buffer
             self.append_clean(L, CleanPage(cid=cid, slot=slot, ku=keep))
         store_kv.clear()

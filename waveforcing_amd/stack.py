@@ -31,12 +31,9 @@ class QuantizedWanStack:
         self.blocks = blocks
         self.exchange = exchange
         # the layers run one after another: one set of activation buffers serves them all
-        shape = {(b.dim, b.ffn_dim, b.device) for b in blocks}
-        if len(shape) == 1:
-            for b in blocks[1:]:
-                b._ws = blocks[0]._ws
+        for b in blocks[1:]:
+            b.share_workspace(blocks[0])
         self.text_kv: list | None = None
-        self._ku: dict[int, torch.Tensor] = {}
 
     @classmethod
     def random(cls, preset: str = "1.3b", n_layers: int | None = None, seed: int = 0, device="cuda",
@@ -72,10 +69,8 @@ class QuantizedWanStack:
                 pool, ctx, own, n_ctx = ex.layer_context(L, csf, qf, height, width, store_kv)
                 ku = None
                 if store and not ex.clean[L]:
-                    # the anchor-to-be: keep its normalized, un-rotated K (promote copies it)
-                    ku = self._ku.get(L)
-                    if ku is None or ku.shape != x.shape:
-                        ku = self._ku[L] = torch.empty_like(x)
+                    # the anchor-to-be (once per stream): keep its normalized, un-rotated K
+                    ku = torch.empty_like(x)
                     store_kv[L] = (store_kv[L][0], ku)
                 blk.forward(x, e, cos, sin, pool, ctx, own, n_ctx, self.text_kv[L], unroped_k_out=ku)
         except BaseException:
