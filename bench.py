@@ -375,7 +375,8 @@ def _cpu_median(fn, reps: int = 5, budget_s: float = 6.0) -> float:
 def cpu_baseline_extra() -> dict:
     """The oracle's torch-CPU path of the other workloads, timed on this host: the int8 W8A8 linear at the
     1.3B shape (whole), the reference's per-tensor e4m3 linear (64 rows) and the attention over 8 chunks
-    (256 queries of one head against all 37440 keys), the last two extrapolated to the full workload."""
+    (256 queries of one head against all 37440 keys), the last two extrapolated to the full workload, and
+    the whole 1.3B block."""
     from oracle import attention as oat
     from oracle import linear as olin
 
@@ -408,7 +409,43 @@ def cpu_baseline_extra() -> dict:
                                  "ms_full_workload_extrapolated": round(full_ms, 1), "cores": threads, "kind": "port",
                                  "sample": "oracle SDPA, 256 queries x 1 head over 37440 keys, fp32; x 219.4 "
                                            "extrapolates to 4680 queries x 12 heads"}
+    out["dit_block_1p3b"] = cpu_baseline_block(threads)
     return out
+
+
+def cpu_baseline_block(threads: int) -> dict:
+    """The oracle's CPU block (oracle.block.block_forward) on the whole 1.3B block workload: 4680 tokens,
+    7 prior chunks + its own of FP8 paged context (37440 keys), 512 text tokens (text K/V outside the timing,
+    as on the GPU), random init; the 30-layer stack figure is 30 x that."""
+    from oracle import block as ob
+    from oracle import kv as okv
+    from waveforcing_amd.block import PRESETS, random_block_params
+
+    cfg = PRESETS["1.3b"]
+    dim, heads, ffn = cfg["dim"], cfg["heads"], cfg["ffn_dim"]
+    frames, h, w = 3, 30, 52
+    T = frames * h * w
+    prior = 7
+    pages = (prior + 1) * frames
+    params = random_block_params(dim, ffn, seed=3)
+    g = torch.Generator().manual_seed(4)
+    pk = okv.new_pool(pages, PAGE, heads, HEAD_DIM)
+    pv = okv.new_pool(pages, PAGE, heads, HEAD_DIM)
+    prior_kv = torch.randn((prior * T, heads, HEAD_DIM), generator=g).to(torch.bfloat16)
+    okv.pack(prior_kv, list(range(prior * frames)), PAGE, *pk)
+    okv.pack(prior_kv, list(range(prior * frames)), PAGE, *pv)
+    del prior_kv
+    text = torch.randn((512, dim), generator=g).to(torch.bfloat16)
+    tk, tv = ob.text_kv(params, text, heads)
+    x = torch.randn((T, dim), generator=g).to(torch.bfloat16)
+    e = (torch.randn((frames, 6, dim), generator=g) * 0.1).to(torch.bfloat16)
+    ctx, own = list(range(pages)), list(range(prior * frames, pages))
+    t = _cpu_median(lambda: ob.block_forward(params, x, e, (frames, h, w), prior * frames, pk, pv, ctx, own,
+                                             (prior + 1) * T, PAGE, tk, tv, heads), reps=3, budget_s=8.0)
+    return {"value": round(t * 1e3, 1), "unit": "ms per block per 3-frame chunk", "higher_is_better": False,
+            "ms_30_layer_stack_extrapolated": round(30 * t * 1e3, 0), "cores": threads, "kind": "port",
+            "sample": "oracle block_forward, whole 1.3B block: 4680 tokens over 37440 FP8 paged keys + 512 text "
+                      "tokens (int8 _int_mm linears, fp32 SDPA)"}
 
 
 def main() -> None:
