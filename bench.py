@@ -283,15 +283,16 @@ def bench_exchange(steps: int, warmup: int, dev: str):
             "gbs": LAYERS * layer_bytes / (ms * 1e-3) / 1e9, "context_keys": n_ctx[0]}
 
 
-def bench_stack(steps: int, warmup: int, dev: str):
-    """One denoise step of the 30 Wan-1.3B blocks over one 3-frame chunk (4680 tokens, 30x52 grid) through
-    the paged exchange at steady state: 8 store passes fill the clean list (anchor + 7), and each timed step
-    is chunk 8's forward (per layer the anchor re-RoPE + pack, the block with its fused K/V pack, attention
-    over anchor + 6 working chunks + self = 37440 keys in a 24-frame window, 512-token text context)."""
+def bench_stack(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
+    """One denoise step of all the Wan blocks of a preset (30 for 1.3B, 40 for 14B) over one 3-frame chunk
+    (4680 tokens, 30x52 grid) through the paged exchange at steady state: 8 store passes fill the clean list
+    (anchor + 7), and each timed step is chunk 8's forward (per layer the anchor re-RoPE + pack, the block
+    with its fused K/V pack, attention over anchor + 6 working chunks + self = 37440 keys in a 24-frame
+    window, 512-token text context)."""
     from waveforcing_amd.stack import QuantizedWanStack
 
     frames, h, w = 3, 30, 52
-    st = QuantizedWanStack.random("1.3b", seed=100, device=dev, tokens_per_frame=h * w, frames_per_chunk=frames,
+    st = QuantizedWanStack.random(preset, seed=100, device=dev, tokens_per_frame=h * w, frames_per_chunk=frames,
                                   max_attn_frames=24)
     dim = st.blocks[0].dim
     g = torch.Generator(device=dev).manual_seed(5)
@@ -311,8 +312,11 @@ def bench_stack(steps: int, warmup: int, dev: str):
         st.forward_chunk(x, e, 8, h, w, store=False)
 
     ms = _timed(step, steps, warmup)
-    return {"ms": ms, "ms_per_layer": ms / len(st.blocks), "layers": len(st.blocks), "tokens": T,
-            "context_keys": n_ctx, "tokens_per_s": T / (ms * 1e-3)}
+    out = {"ms": ms, "ms_per_layer": ms / len(st.blocks), "layers": len(st.blocks), "tokens": T,
+           "context_keys": n_ctx, "tokens_per_s": T / (ms * 1e-3)}
+    del st, x, x0
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_copy(steps: int, warmup: int, dev: str):
@@ -458,7 +462,7 @@ def main() -> None:
     ap.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
                     help="minimum untimed warm-up of the KV workloads (profiler runs use 0)")
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
-                                       "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "copy"],
+                                       "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -476,7 +480,7 @@ def main() -> None:
               "linears_1p3b": bench_block_linears, "attention": bench_attention, "copy": bench_copy,
               "block_1p3b": lambda s, w, d: bench_block("1.3b", s, w, d),
               "block_14b": lambda s, w, d: bench_block("14b", s, w, d), "exchange_1p3b": bench_exchange,
-              "stack_1p3b": bench_stack,
+              "stack_1p3b": bench_stack, "stack_14b": lambda s, w, d: bench_stack(s, w, d, "14b"),
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
@@ -489,6 +493,7 @@ def main() -> None:
     b14 = bench_block("14b", max(3, args.steps // 10), 1, dev)
     xch = bench_exchange(max(5, args.steps // 5), 2, dev)
     stk = bench_stack(max(3, args.steps // 10), 1, dev)
+    stk14 = bench_stack(3, 1, dev, "14b")
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     cpu_extra = None if args.no_cpu_baseline else cpu_baseline_extra()
     # one launch per step: the launch duration is the step time
@@ -563,7 +568,9 @@ def main() -> None:
             "dit_stack_1p3b_ms_per_chunk": round(stk["ms"], 3),
             "dit_stack_1p3b_ms_per_layer": round(stk["ms_per_layer"], 4),
             "dit_stack_1p3b_tokens_per_s": round(stk["tokens_per_s"], 1),
-            "dit_stack_note": "30 blocks of Wan-1.3B over one 4680-token chunk, one denoise step at steady state "
+            "dit_stack_14b_ms_per_chunk": round(stk14["ms"], 2),
+            "dit_stack_14b_ms_per_layer": round(stk14["ms_per_layer"], 3),
+            "dit_stack_note": "30 blocks of Wan-1.3B (40 of 14B) over one 4680-token chunk, one denoise step at steady state "
                               "through the paged exchange (anchor re-RoPE + fused in-block K/V pack per layer, "
                               "37440-key context), random init drawn on the GPU",
             "dit_block_1p3b_ms_per_chunk": round(b13["ms"], 4),
