@@ -144,6 +144,14 @@ def _gate_residual(x, y, gate, frame_tokens):
               gate.stride(0) if gate is not None else 0, T, dim, frame_tokens, _lib.stream_handle(x.device))
 
 
+def apply_pending_residual(x: torch.Tensor, pending, frame_tokens: int) -> torch.Tensor:
+    """x = bf16(x + bf16(y * gate)) in place for the (y, gate) a block's forward(defer_residual=True)
+    returned: the block's last gated residual (causal_model.py:397-398)."""
+    y, gate = pending
+    _gate_residual(x, y, gate, frame_tokens)
+    return x
+
+
 def _linear_i8(x, lin: QLinear, ws_q, ws_s, out, gelu=False):
     """W8A8 linear of bf16 x [M, K] into out [M, N] via the fused C entry point."""
     M, K = x.shape
@@ -246,7 +254,8 @@ class QuantizedWanBlock:
 
     def forward(self, x: torch.Tensor, e: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pool: Fp8PagePool,
                 context_table: PageTable, own_table: PageTable, n_context: int, text_kv,
-                unroped_k_out: torch.Tensor | None = None) -> torch.Tensor:
+                unroped_k_out: torch.Tensor | None = None, es: torch.Tensor | None = None, pending=None,
+                defer_residual: bool = False):
         """Advance x [T, dim] bf16 in place through the block.
 
         e: [F, 6, dim] bf16 time modulation of the chunk's F frames.
@@ -256,6 +265,16 @@ class QuantizedWanBlock:
         including this chunk's T tokens, which are packed into own_table here.
         unroped_k_out: optional [T, dim] bf16 buffer for this chunk's normalized,
         un-rotated K (the exchange's unroped_key, kept for the anchor re-RoPE).
+        es: optional precomputed bf16 ``modulation + e`` [F, 6, dim] of this block
+        (a stack adds every layer's table in one launch).
+        pending: optional (y, gate) residual left by the previous block's
+        ``defer_residual``; it is applied in front of this block's first
+        LayerNorm, in the same kernel, with the same arithmetic as a separate
+        wf_gate_residual.
+        defer_residual: leave this block's last gated residual undone and return
+        (x, (y, gate)) for the next block (or apply_pending_residual); y is this
+        block's workspace, valid until the next forward of a block sharing it
+        has run its first LayerNorm.
         """
         T, dim = x.shape
         F = e.shape[0]
@@ -266,12 +285,18 @@ class QuantizedWanBlock:
         ws = self._workspace(T)
         # e = (modulation + e).chunk(6)  (causal_model.py:376), bf16: one add; the kernels read
         # the six [F, dim] chunks as strided frame rows of it.
-        es = self.modulation[0].unsqueeze(0) + e
+        if es is None:
+            es = self.modulation[0].unsqueeze(0) + e
+        elif es.shape != (F, 6, dim):
+            raise ValueError(f"es must be [{F}, 6, {dim}], got {tuple(es.shape)}")
         e0, e1, e2, e3, e4, e5 = (es[:, i] for i in range(6))
         aq, as_ = ws["aq"], ws["as_"]
 
         # self-attention: LN1 + modulation + int8 quant -> fused QKV
-        _ln_quant(x, dim, ft, aq, as_, shift=e0, scale=e1)
+        if pending is None:
+            _ln_quant(x, dim, ft, aq, as_, shift=e0, scale=e1)
+        else:  # the previous block's last gated residual, fused in front of LN1
+            _ln_quant(x, dim, ft, aq, as_, shift=e0, scale=e1, res_y=pending[0], res_gate=pending[1])
         gemm_i8(aq, self.qkv.w, as_, self.qkv.s, self.qkv.b, out=ws["qkv"])
         qkv = ws["qkv"]
         q, k, v = qkv[:, :dim], qkv[:, dim:2 * dim], qkv[:, 2 * dim:]
@@ -295,5 +320,7 @@ class QuantizedWanBlock:
         _ln_quant(x, dim, ft, aq, as_, shift=e3, scale=e4, res_y=ws["y"])
         gemm_i8(aq, self.fc_in.w, as_, self.fc_in.s, self.fc_in.b, gelu=True, out=ws["ffn"])
         _linear_i8(ws["ffn"], self.fc_out, ws["fq"], as_, ws["y"])
+        if defer_residual:
+            return x, (ws["y"], e5)
         _gate_residual(x, ws["y"], e5, ft)
         return x

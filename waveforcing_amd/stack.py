@@ -18,7 +18,7 @@ from __future__ import annotations
 import torch
 
 from . import rope
-from .block import PRESETS, QuantizedWanBlock, random_block_params
+from .block import PRESETS, QuantizedWanBlock, apply_pending_residual, random_block_params
 from .exchange import PagedExchange
 
 
@@ -33,6 +33,8 @@ class QuantizedWanStack:
         # the layers run one after another: one set of activation buffers serves them all
         for b in blocks[1:]:
             b.share_workspace(blocks[0])
+        # every layer's modulation table, so one add per chunk forms all the ``modulation + e``
+        self._modulation = torch.stack([b.modulation[0] for b in blocks])   # [L, 6, dim]
         self.text_kv: list | None = None
 
     @classmethod
@@ -55,7 +57,8 @@ class QuantizedWanStack:
         """Advance x [T, dim] bf16 in place through every layer for chunk ``chunk`` (latent frames
         chunk * npb ...).  A denoise step (store=False) releases the chunk's slots at the end; a store
         pass (store=True) keeps its K/V in their slots and adds them to every layer's clean list,
-        the first such chunk becoming the anchor with its un-rotated K kept for re-RoPE."""
+        the first such chunk becoming the anchor with its un-rotated K kept for re-RoPE.  On an error x
+        is left partly updated and the chunk's slots are returned."""
         if self.text_kv is None:
             raise RuntimeError("set_text() first")
         ex = self.exchange
@@ -64,6 +67,8 @@ class QuantizedWanStack:
         csf = chunk * npb
         cos, sin = rope.cos_sin(npb, height, width, csf, ex.head_dim, device=x.device)
         store_kv: dict | None = {} if store else None
+        es_all = self._modulation.unsqueeze(1) + e.unsqueeze(0)   # [L, F, 6, dim], one bf16 add
+        pending = None
         try:
             for L, blk in enumerate(self.blocks):
                 pool, ctx, own, n_ctx = ex.layer_context(L, csf, qf, height, width, store_kv)
@@ -72,7 +77,10 @@ class QuantizedWanStack:
                     # the anchor-to-be (once per stream): keep its normalized, un-rotated K
                     ku = torch.empty_like(x)
                     store_kv[L] = (store_kv[L][0], ku)
-                blk.forward(x, e, cos, sin, pool, ctx, own, n_ctx, self.text_kv[L], unroped_k_out=ku)
+                # each block's last gated residual runs fused into the next block's first LayerNorm
+                x, pending = blk.forward(x, e, cos, sin, pool, ctx, own, n_ctx, self.text_kv[L], unroped_k_out=ku,
+                                         es=es_all[L], pending=pending, defer_residual=True)
+            apply_pending_residual(x, pending, x.shape[0] // e.shape[0])
         except BaseException:
             if store:
                 ex.abort_store(store_kv)
