@@ -306,6 +306,24 @@ int wf_gate_residual(void* x, int64_t ldx, const void* y, int64_t ldy,
                      const void* gate, int64_t ld_gate, int64_t T,
                      int32_t dim, int32_t frame_tokens, void* stream);
 
+/* wf_k_norm_rope_kv_pack with Q done in the same pass: Q [n_tokens][ld_q]
+ * (the Q columns of the fused QKV output) gets
+ * bf16(bf16(q * rsqrt(mean(q^2) + eps)) * norm_q) and the same rotation as
+ * K, written back in place; bit-identical to wf_rmsnorm_rope on Q followed by
+ * wf_k_norm_rope_kv_pack.  The self-attention q/k RMSNorm + RoPE and K/V
+ * publish of one layer (causal_model.py:112-116, wave_rt/runtime/
+ * backend.py:119-121, paged.py:215-237) in one launch.  q must not overlap
+ * K, V or ku_out (interleaved column slices of one QKV row are fine). */
+int wf_qk_norm_rope_kv_pack(void* q, int64_t ld_q, const void* norm_q,
+                            const void* k, const void* v, int64_t n_tokens,
+                            int32_t n_heads, int32_t head_dim, int64_t ld_kv,
+                            float eps, const void* norm_k, const float* cos,
+                            const float* sin, void* ku_out, int64_t ld_ku,
+                            const int32_t* page_table, int64_t n_table,
+                            int32_t page_tokens, uint8_t* k_codes,
+                            uint8_t* v_codes, float* k_scales,
+                            float* v_scales, int64_t pool_pages, void* stream);
+
 /* ---------------------------------------------------------------------
  * Re-noising for the next DMD step
  * ------------------------------------------------------------------- */

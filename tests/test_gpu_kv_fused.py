@@ -195,3 +195,48 @@ def test_fused_pack_argument_errors():
     with pytest.raises(ValueError, match="rope cos"):
         pool.pack(k.view(20, 2, 128), None, table, rope=(cos[:10], cos[:10]))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T,H,page,P,start,seed", [
+    (4680, 12, 1560, 6, 6, 0),     # 1.3B (one wave per row)
+    (4680, 40, 1560, 4, 3, 1),     # 14B (one workgroup per row: the q reduction has its own LDS slots)
+    (40, 128, 16, 4, 5, 3),        # 16384-wide rows
+])
+def test_qk_norm_rope_pack_equals_separate_q_pass(T, H, page, P, start, seed):
+    dim = H * 128
+    qkv, w = _qkv(T, dim, seed)
+    wq = (1 + 0.1 * torch.randn((dim,), generator=torch.Generator().manual_seed(seed + 50))).to(torch.bfloat16)
+    cos, sin = _tables(T, start)
+    ids = inputs.page_table(-(-T // page), P, seed=seed)
+    a = qkv.to(DEV)
+    b = qkv.to(DEV)
+    wd, wqd = w.to(DEV), wq.to(DEV)
+    ku_a = torch.empty((T, dim), dtype=torch.bfloat16, device=DEV)
+    ku_b = torch.empty_like(ku_a)
+    fused = Fp8PagePool(P, H, 128, page, DEV)
+    fused.pack_k_norm_rope(a[:, dim:2 * dim], a[:, 2 * dim:], fused.page_table(ids), wd, EPS, (cos, sin), ku_out=ku_a,
+                           q=a[:, :dim], norm_q=wqd)
+    ref = Fp8PagePool(P, H, 128, page, DEV)
+    qb = b[:, :dim]
+    _lib.call("wf_rmsnorm_rope", qb.data_ptr(), T, dim, qb.stride(0), 128, EPS, wqd.data_ptr(), cos.data_ptr(),
+              sin.data_ptr(), qb.data_ptr(), qb.stride(0), _lib.stream_handle(DEV))
+    ref.pack_k_norm_rope(b[:, dim:2 * dim], b[:, 2 * dim:], ref.page_table(ids), wd, EPS, (cos, sin), ku_out=ku_b)
+    assert torch.equal(a, b)                         # q rewritten identically, K and V untouched
+    assert torch.equal(ku_a, ku_b)
+    for x, y in zip(_pools_cpu(fused), _pools_cpu(ref)):
+        assert torch.equal(x, y)
+
+
+def test_qk_norm_rope_pack_rejects_overlapping_q():
+    T, H, page = 8, 2, 16
+    dim = H * 128
+    d = torch.zeros((T, 3 * dim), dtype=torch.bfloat16, device=DEV)
+    w = torch.ones((dim,), dtype=torch.bfloat16, device=DEV)
+    pool = Fp8PagePool(2, H, 128, page, DEV)
+    table = pool.page_table([0])
+    k = d[:, dim:2 * dim]
+    with pytest.raises(RuntimeError, match="must not overlap"):
+        pool.pack_k_norm_rope(k, None, table, w, EPS, None, q=d[:, dim - 64:2 * dim - 64], norm_q=w)
+    with pytest.raises(ValueError, match="norm_q"):
+        pool.pack_k_norm_rope(k, None, table, w, EPS, None, q=d[:, :dim])
+    torch.cuda.synchronize()

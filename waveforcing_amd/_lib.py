@@ -47,6 +47,14 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
         _c_void_p,
     ],
+    "wf_qk_norm_rope_kv_pack": [
+        _c_void_p, _i64, _c_void_p,
+        _c_void_p, _c_void_p, _i64, _i32, _i32, _i64,
+        _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+        _c_void_p, _i64, _i32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+        _c_void_p,
+    ],
     "wf_fp8_kv_unpack": [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
         _c_void_p, _i64, _i32, _i64, _i32, _i32,

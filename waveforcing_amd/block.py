@@ -300,10 +300,10 @@ class QuantizedWanBlock:
         gemm_i8(aq, self.qkv.w, as_, self.qkv.s, self.qkv.b, out=ws["qkv"])
         qkv = ws["qkv"]
         q, k, v = qkv[:, :dim], qkv[:, dim:2 * dim], qkv[:, 2 * dim:]
-        # in place: each row is read whole before its reduction, written after
-        _rmsnorm_rope(q, hd, self.norm_q, cos, sin, q)
-        # K: RMSNorm + RoPE + FP8 pack into this chunk's pages, V packed beside it
-        pool.pack_k_norm_rope(k, v, own_table, self.norm_k, EPS, (cos, sin), ku_out=unroped_k_out)
+        # q and K: RMSNorm + RoPE in one pass (q in place: each row is read whole before it is
+        # written), K FP8-packed into this chunk's pages and V packed beside it
+        pool.pack_k_norm_rope(k, v, own_table, self.norm_k, EPS, (cos, sin), ku_out=unroped_k_out, q=q,
+                              norm_q=self.norm_q)
         ctx = PagedKV(pool, context_table, n_context)
         attn_paged_fp8(q.view(T, H, hd), ctx, out=ws["attn"].view(T, H, hd))
         _linear_i8(ws["attn"], self.o, aq, as_, ws["y"])

@@ -231,6 +231,9 @@ struct KNormPackArgs {
   const float* sin;
   uint16_t* ku;         // normalized, un-rotated K [T][ld_ku] bf16, or null
   int64_t ld_ku;
+  uint16_t* q;          // Q [T][ld_q] bf16, RMSNorm'd (weight wq) and rotated in place, or null
+  int64_t ld_q;
+  const uint16_t* wq;
   PageGeom geom;
   PoolView kpool, vpool;
 };
@@ -276,7 +279,7 @@ __device__ inline void pack_head_chunk(const float* y, int ch, bool valid, bool 
 template <int LPR, int NC>
 __global__ __launch_bounds__(256) void k_norm_rope_pack_kernel(KNormPackArgs a) {
   constexpr int RPB = 256 / LPR;
-  __shared__ float red[4];
+  __shared__ float red[4], redq[4];
   // Row blocks go XCD-contiguously (as block_of), so the token-fastest scale
   // lines of neighbouring tokens are written through one L2.
   const uint32_t n_blk = (static_cast<uint32_t>(a.T) + RPB - 1) / RPB;
@@ -307,6 +310,17 @@ __global__ __launch_bounds__(256) void k_norm_rope_pack_kernel(KNormPackArgs a) 
     for (int c = 0; c < NC; ++c) {
       const int ch = lane + LPR * c;
       vw[c] = ch < n_chunks ? rows::ld16(vrow + ch * 8) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  uint4 qw[NC], wqw[NC];
+  uint16_t* qrow = a.q ? a.q + static_cast<int64_t>(t) * a.ld_q : nullptr;
+  if (a.q) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int ch = lane + LPR * c;
+      const bool valid = ch < n_chunks;
+      qw[c] = valid ? rows::ld16(qrow + ch * 8) : make_uint4(0, 0, 0, 0);
+      wqw[c] = valid ? rows::ld16(a.wq + ch * 8) : make_uint4(0, 0, 0, 0);
     }
   }
   int64_t code_row0 = 0, scale0 = 0;
@@ -345,6 +359,35 @@ __global__ __launch_bounds__(256) void k_norm_rope_pack_kernel(KNormPackArgs a) 
       float y[8];
       rows::unpack8(vw[c], y);
       pack_head_chunk(y, ch, ch < n_chunks, placed, a.geom, code_row0, scale0, a.vpool);
+    }
+  }
+  if (a.q) {
+    // Q: the same RMSNorm (its own weight) and rotation, written back in place
+    // (the row was read whole above); wf_rmsnorm_rope's arithmetic
+    float sqq = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float x[8];
+      rows::unpack8(qw[c], x);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sqq += x[i] * x[i];
+    }
+    const float msq = rows::row_sum<LPR>(sqq, redq) / static_cast<float>(n_chunks * 8);
+    const float rq = 1.0f / sqrtf(msq + a.eps);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int ch = lane + LPR * c;
+      float x[8], wv[8];
+      rows::unpack8(qw[c], x);
+      rows::unpack8(wqw[c], wv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = x[i] * rq;
+      rows::rbf8(x);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = x[i] * wv[i];
+      rows::rbf8(x);
+      if (rot) rope4_bf16(x, cs[c], sn[c]);
+      if (ch < n_chunks) rows::st16(qrow + ch * 8, rows::pack8(x));
     }
   }
 }
@@ -453,32 +496,23 @@ int launch_pack(const char* fn, const void* k, const void* v, int64_t n_tokens, 
 }  // namespace
 }  // namespace wf
 
-extern "C" {
-
-int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
-                   int64_t ld_kv, const int32_t* page_table, int64_t n_table, int32_t page_tokens, uint8_t* k_codes,
-                   uint8_t* v_codes, float* k_scales, float* v_scales, int64_t pool_pages, void* stream) {
-  return wf::launch_pack("wf_fp8_kv_pack", k, v, n_tokens, n_heads, head_dim, ld_kv, nullptr, nullptr, page_table,
-                         n_table, page_tokens, k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
+namespace wf {
+namespace {
+// Rows [T][dim] at a (stride lda) and at b (stride ldb) share no element.
+bool rows_disjoint(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t T, int64_t dim) {
+  const int64_t d = (reinterpret_cast<intptr_t>(b) - reinterpret_cast<intptr_t>(a)) / 2;  // bf16 elements
+  const int64_t span_a = (T - 1) * lda + dim, span_b = (T - 1) * ldb + dim;
+  if (d >= span_a || -d >= span_b) return true;
+  if (lda != ldb || (reinterpret_cast<intptr_t>(b) - reinterpret_cast<intptr_t>(a)) % 2) return false;
+  const int64_t r = ((d % lda) + lda) % lda;  // interleaved rows, e.g. column slices of one QKV output
+  return r >= dim && r <= lda - dim;
 }
 
-int wf_fp8_kv_pack_rope(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
-                        int64_t ld_kv, const float* cos, const float* sin, const int32_t* page_table, int64_t n_table,
-                        int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales, float* v_scales,
-                        int64_t pool_pages, void* stream) {
-  static const char* fn = "wf_fp8_kv_pack_rope";
-  WF_REQUIRE(n_tokens == 0 || (cos && sin), WF_E_INVALID, "%s: null RoPE table", fn);
-  WF_REQUIRE(wf::aligned16(cos) && wf::aligned16(sin), WF_E_ALIGN, "%s: RoPE tables must be 16-byte aligned", fn);
-  return wf::launch_pack(fn, k, v, n_tokens, n_heads, head_dim, ld_kv, cos, sin, page_table, n_table, page_tokens,
-                         k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
-}
-
-int wf_k_norm_rope_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
-                           int64_t ld_kv, float eps, const void* norm_w, const float* cos, const float* sin,
-                           void* ku_out, int64_t ld_ku, const int32_t* page_table, int64_t n_table,
-                           int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales, float* v_scales,
-                           int64_t pool_pages, void* stream) {
-  static const char* fn = "wf_k_norm_rope_kv_pack";
+int k_norm_pack(const char* fn, void* q, int64_t ld_q, const void* norm_q, const void* k, const void* v,
+                int64_t n_tokens, int32_t n_heads, int32_t head_dim, int64_t ld_kv, float eps, const void* norm_w,
+                const float* cos, const float* sin, void* ku_out, int64_t ld_ku, const int32_t* page_table,
+                int64_t n_table, int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales,
+                float* v_scales, int64_t pool_pages, void* stream) {
   if (int st = wf::check_pool_args(fn, n_tokens, n_heads, head_dim, page_table, n_table, page_tokens, pool_pages))
     return st;
   if (n_tokens == 0) return WF_OK;
@@ -510,6 +544,13 @@ int wf_k_norm_rope_kv_pack(const void* k, const void* v, int64_t n_tokens, int32
       WF_REQUIRE(ub + span_u <= vb || vb + span_k <= ub, WF_E_INVALID, "%s: ku_out overlaps V", fn);
     }
   }
+  if (q) {
+    WF_REQUIRE(norm_q && ld_q >= dim && ld_q % 8 == 0 && wf::aligned16(q) && wf::aligned16(norm_q), WF_E_INVALID,
+               "%s: q needs its weight, ld_q >= n_heads*head_dim with ld_q %% 8 == 0 and 16-byte alignment", fn);
+    WF_REQUIRE(rows_disjoint(q, ld_q, k, ld_kv, n_tokens, dim) && (!v || rows_disjoint(q, ld_q, v, ld_kv, n_tokens, dim)) &&
+                   (!ku_out || rows_disjoint(q, ld_q, ku_out, ld_ku, n_tokens, dim)),
+               WF_E_INVALID, "%s: q must not overlap K, V or ku_out", fn);
+  }
   wf::KNormPackArgs a;
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
@@ -521,6 +562,9 @@ int wf_k_norm_rope_kv_pack(const void* k, const void* v, int64_t n_tokens, int32
   a.sin = sin;
   a.ku = static_cast<uint16_t*>(ku_out);
   a.ld_ku = ld_ku;
+  a.q = static_cast<uint16_t*>(q);
+  a.ld_q = ld_q;
+  a.wq = static_cast<const uint16_t*>(norm_q);
   a.geom = wf::make_geom(n_heads, page_table, n_table, page_tokens, pool_pages);
   a.kpool = wf::PoolView{k_codes, k_scales};
   a.vpool = wf::PoolView{v_codes, v_scales};
@@ -531,6 +575,51 @@ int wf_k_norm_rope_kv_pack(const void* k, const void* v, int64_t n_tokens, int32
                        0, wf::as_stream(stream), a);
   });
   return wf::check_launch(fn);
+}
+}  // namespace
+}  // namespace wf
+
+extern "C" {
+
+int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
+                   int64_t ld_kv, const int32_t* page_table, int64_t n_table, int32_t page_tokens, uint8_t* k_codes,
+                   uint8_t* v_codes, float* k_scales, float* v_scales, int64_t pool_pages, void* stream) {
+  return wf::launch_pack("wf_fp8_kv_pack", k, v, n_tokens, n_heads, head_dim, ld_kv, nullptr, nullptr, page_table,
+                         n_table, page_tokens, k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
+}
+
+int wf_fp8_kv_pack_rope(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
+                        int64_t ld_kv, const float* cos, const float* sin, const int32_t* page_table, int64_t n_table,
+                        int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales, float* v_scales,
+                        int64_t pool_pages, void* stream) {
+  static const char* fn = "wf_fp8_kv_pack_rope";
+  WF_REQUIRE(n_tokens == 0 || (cos && sin), WF_E_INVALID, "%s: null RoPE table", fn);
+  WF_REQUIRE(wf::aligned16(cos) && wf::aligned16(sin), WF_E_ALIGN, "%s: RoPE tables must be 16-byte aligned", fn);
+  return wf::launch_pack(fn, k, v, n_tokens, n_heads, head_dim, ld_kv, cos, sin, page_table, n_table, page_tokens,
+                         k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
+}
+
+
+int wf_k_norm_rope_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
+                           int64_t ld_kv, float eps, const void* norm_w, const float* cos, const float* sin,
+                           void* ku_out, int64_t ld_ku, const int32_t* page_table, int64_t n_table,
+                           int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales, float* v_scales,
+                           int64_t pool_pages, void* stream) {
+  return wf::k_norm_pack("wf_k_norm_rope_kv_pack", nullptr, 0, nullptr, k, v, n_tokens, n_heads, head_dim, ld_kv, eps,
+                         norm_w, cos, sin, ku_out, ld_ku, page_table, n_table, page_tokens, k_codes, v_codes, k_scales,
+                         v_scales, pool_pages, stream);
+}
+
+int wf_qk_norm_rope_kv_pack(void* q, int64_t ld_q, const void* norm_q, const void* k, const void* v, int64_t n_tokens,
+                            int32_t n_heads, int32_t head_dim, int64_t ld_kv, float eps, const void* norm_k,
+                            const float* cos, const float* sin, void* ku_out, int64_t ld_ku,
+                            const int32_t* page_table, int64_t n_table, int32_t page_tokens, uint8_t* k_codes,
+                            uint8_t* v_codes, float* k_scales, float* v_scales, int64_t pool_pages, void* stream) {
+  static const char* fn = "wf_qk_norm_rope_kv_pack";
+  WF_REQUIRE(q != nullptr, WF_E_INVALID, "%s: null q (use wf_k_norm_rope_kv_pack without q)", fn);
+  return wf::k_norm_pack(fn, q, ld_q, norm_q, k, v, n_tokens, n_heads, head_dim, ld_kv, eps, norm_k, cos, sin, ku_out,
+                         ld_ku, page_table, n_table, page_tokens, k_codes, v_codes, k_scales, v_scales, pool_pages,
+                         stream);
 }
 
 int wf_fp8_kv_unpack(const uint8_t* k_codes, const uint8_t* v_codes, const float* k_scales, const float* v_scales,

@@ -158,7 +158,8 @@ class Fp8PagePool:
 
     def pack_k_norm_rope(self, k: torch.Tensor, v: torch.Tensor | None, table: PageTable, norm_w: torch.Tensor,
                          eps: float, rope: tuple[torch.Tensor, torch.Tensor] | None,
-                         ku_out: torch.Tensor | None = None) -> None:
+                         ku_out: torch.Tensor | None = None, q: torch.Tensor | None = None,
+                         norm_q: torch.Tensor | None = None) -> None:
         """K straight from the QKV projection into the pages.
 
         k, v: [T, dim] bf16 rows (dim = H*D, token stride a multiple of 8, e.g.
@@ -166,9 +167,11 @@ class Fp8PagePool:
         (norm_w [dim]), is written un-rotated to ``ku_out`` ([T, dim] bf16, may
         be ``k`` itself) if given, is rotated by ``rope = (cos, sin)`` and is
         packed; V is packed as by :meth:`pack`.  Equal, bit for bit, to
-        wf_rmsnorm_rope followed by wf_fp8_kv_pack.
+        wf_rmsnorm_rope followed by wf_fp8_kv_pack.  With ``q`` (and its
+        RMSNorm weight ``norm_q``), Q's RMSNorm + RoPE runs in the same pass,
+        in place (wf_qk_norm_rope_kv_pack).
         """
-        for name, t in (("k", k), ("v", v), ("ku_out", ku_out)):
+        for name, t in (("k", k), ("v", v), ("ku_out", ku_out), ("q", q)):
             if t is None:
                 continue
             if t.dim() != 2 or t.dtype != torch.bfloat16 or t.stride(1) != 1:
@@ -181,14 +184,17 @@ class Fp8PagePool:
             raise ValueError("v must match k's shape and token stride")
         if ku_out is not None and tuple(ku_out.shape) != (T, dim):
             raise ValueError("ku_out must be [T, dim]")
+        if q is not None and (tuple(q.shape) != (T, dim) or norm_q is None):
+            raise ValueError("q must be [T, dim] and comes with norm_q")
         if len(table) * self.page_tokens < T:
             raise RuntimeError(f"page table of {len(table)} pages cannot hold {T} tokens")
         cos = sin = None
         if rope is not None:
             cos, sin = _rope_tables(rope, T, D, self.device)
         ld = k.stride(0) if T > 1 else dim
+        qargs = () if q is None else (q.data_ptr(), q.stride(0) if T > 1 else dim, norm_q.data_ptr())
         _lib.call(
-            "wf_k_norm_rope_kv_pack",
+            "wf_k_norm_rope_kv_pack" if q is None else "wf_qk_norm_rope_kv_pack", *qargs,
             k.data_ptr(), _lib.ptr(v), T, H, D, ld, float(eps), norm_w.data_ptr(), _lib.ptr(cos), _lib.ptr(sin),
             _lib.ptr(ku_out), (ku_out.stride(0) if T > 1 else dim) if ku_out is not None else 0,
             table.dev.data_ptr(), len(table), self.page_tokens,
