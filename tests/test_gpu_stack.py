@@ -58,11 +58,11 @@ def _stack(params):
     return st
 
 
-def _list_context(clean, csf):
+def _list_context(clean, csf, qf=NPB):
     """(anchor cid or None, anchor rope start, working cids) of the clean list model."""
     if not clean:
         return None, None, []
-    _, n_w = ex.anchor_and_working(len(clean), ex.working_chunks(WINDOW, NPB, NPB))
+    _, n_w = ex.anchor_and_working(len(clean), ex.working_chunks(WINDOW, qf, NPB))
     working = clean[len(clean) - n_w:] if n_w else []
     return clean[0], ex.anchor_rope_start(csf, len(working), NPB), working
 
@@ -75,7 +75,8 @@ def _pages(c):
     return list(range(NPB * c, NPB * c + NPB))
 
 
-def test_stack_equals_manual_replay_over_ten_chunks():
+@pytest.mark.parametrize("qf", [NPB, 2 * NPB])   # one query chunk (2 working chunks) or two (1)
+def test_stack_equals_manual_replay_over_ten_chunks(qf):
     params = _params()
     st = _stack(params)
     blocks = st.blocks
@@ -90,11 +91,12 @@ def test_stack_equals_manual_replay_over_ten_chunks():
         cos, sin = rope.cos_sin(NPB, HT, WD, csf, device=DEV)
         for store in (False, True):
             x, e = _inputs(c, store)
-            got = st.forward_chunk(x.to(DEV).clone(), e.to(DEV), c, HT, WD, store=store)
+            q = NPB if store else qf     # store passes carry one chunk (paged.py:257-310)
+            got = st.forward_chunk(x.to(DEV).clone(), e.to(DEV), c, HT, WD, store=store, query_frames=q)
             want = x.to(DEV).clone()
             for L, blk in enumerate(blocks):
                 pool = pools[L]
-                anchor, start, working = _list_context(clean[L], csf)
+                anchor, start, working = _list_context(clean[L], csf, q)
                 ctx_pages = []
                 if anchor is not None:
                     acos, asin = rope.cos_sin(NPB, HT, WD, start, device=DEV)

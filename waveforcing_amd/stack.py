@@ -63,7 +63,8 @@ class QuantizedWanStack:
             raise RuntimeError("set_text() first")
         ex = self.exchange
         npb = ex.npb
-        qf = npb if query_frames is None else query_frames
+        # a store pass's context geometry is one chunk's (make_store_exch, paged.py:257-310)
+        qf = npb if (store or query_frames is None) else query_frames
         csf = chunk * npb
         cos, sin = rope.cos_sin(npb, height, width, csf, ex.head_dim, device=x.device)
         store_kv: dict | None = {} if store else None
