@@ -247,74 +247,111 @@ def bench_block(scale: str, steps: int, warmup: int, dev: str):
     return {"ms": ms, "tokens": T, "context_keys": (prior + 1) * T}
 
 
-def bench_exchange(steps: int, warmup: int, dev: str):
-    """One denoise step's paged exchange over the 30 Wan-1.3B layers at steady state: per layer,
-    pack this chunk's K/V into its slot and re-RoPE + pack the anchor's K, with a full clean list
-    (anchor + 7) and a 24-frame window (anchor + 6 working chunks + self = 37440 keys)."""
-    from waveforcing_amd.exchange import CleanPage, PagedExchange
+def _prefill_clean(x, filler, n_clean: int = 8) -> None:
+    """Fill every layer's clean list of exchange ``x`` with ``n_clean`` chunks of ``filler`` K/V (slots packed
+    directly), the first one the anchor with ``filler`` as its un-rotated K."""
+    from waveforcing_amd.exchange import CleanPage
 
-    x = PagedExchange(LAYERS, HEADS, PAGE, frames_per_chunk=3, max_attn_frames=24, device=dev)
-    g = torch.Generator().manual_seed(21)
-    filler = torch.randn((TOKENS, HEADS, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
-    for layer in range(LAYERS):
-        for cid in range(8):
+    for layer in range(x.n_layers):
+        for cid in range(n_clean):
             slot = x.reserve(layer)
             x.pack(layer, slot, filler, filler)
-            x.append_clean(layer, CleanPage(cid, slot, ku=filler.clone() if cid == 0 else None))
+            x.append_clean(layer, CleanPage(cid, slot))
+    x.anchor_ku = filler.unsqueeze(0).expand(x.n_layers, *filler.shape).contiguous()
+
+
+STEADY_TICK = 12  # rf_step 4 with 8 clean chunks (0..7): the store rank stores chunk 8, ranks 0..3 hold 12..9
+
+
+def bench_exchange(steps: int, warmup: int, dev: str):
+    """The paged exchange of one steady-state wavefront tick over the 30 Wan-1.3B layers (rf_step 4, 21-frame
+    window, clean list anchor + 7): the store pass and the four denoise passes each pack their chunk's K/V into
+    its slot per layer, and the anchor's K is re-RoPEd for the store geometry and for the denoise geometry (one
+    launch over all layers each).  Rank 0's context is anchor + 2 working + live + self + 3 in-flight = 37440
+    keys."""
+    from waveforcing_amd.exchange import PagedExchange, TickPlan
+
+    x = PagedExchange(LAYERS, HEADS, PAGE, frames_per_chunk=3, max_attn_frames=21, rf_step=4, device=dev)
+    g = torch.Generator().manual_seed(21)
+    filler = torch.randn((TOKENS, HEADS, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    _prefill_clean(x, filler)
     k, v = inputs.kv_layer(0)
     k, v = k.to(dev).unsqueeze(0), v.to(dev).unsqueeze(0)
+    plan = TickPlan(STEADY_TICK, [0, 1, 2, 3], True, (STEADY_TICK - 3) * 3, 12)
     n_ctx = []
 
     def step():
-        exch = x.make_denoise_exch(8 * 3)
-        for layer in range(LAYERS):
-            ctx, _ = exch(layer_idx=layer, roped_query=None, roped_key=k, unroped_key=None, value=v,
-                          post_patch_height=30, post_patch_width=52)
-            if not n_ctx:
-                n_ctx.append(ctx.n_tokens)
-        x.finish_denoise()
+        x.begin_tick(plan)
+        for exch in [x.make_store_exch()] + [x.make_denoise_exch(r) for r in (3, 2, 1, 0)]:
+            for layer in range(LAYERS):
+                ctx, _ = exch(layer_idx=layer, roped_query=None, roped_key=k, unroped_key=None, value=v,
+                              post_patch_height=30, post_patch_width=52)
+        n_ctx.append(ctx.n_tokens)
+        x.abort_tick()   # keep the clean lists as they are: every timed tick is the same steady-state tick
 
     ms = _timed(step, steps, warmup)
     elems = TOKENS * HEADS * HEAD_DIM
     rows = TOKENS * HEADS
-    anchor_bytes = elems * 2 + elems + rows * 4          # K only: read bf16, write codes + scales
-    layer_bytes = kv_bytes_per_layer() + anchor_bytes
-    return {"ms": ms, "us_per_layer": ms * 1e3 / LAYERS, "bytes_per_layer": layer_bytes,
-            "gbs": LAYERS * layer_bytes / (ms * 1e-3) / 1e9, "context_keys": n_ctx[0]}
+    anchor_bytes = LAYERS * (elems * 2 + elems + rows * 4)   # K only: read bf16, write codes + scales
+    tick_bytes = 5 * LAYERS * kv_bytes_per_layer() + 2 * anchor_bytes
+    return {"ms_per_tick": ms, "us_per_pass_layer": ms * 1e3 / (5 * LAYERS), "bytes_per_tick": tick_bytes,
+            "gbs": tick_bytes / (ms * 1e-3) / 1e9, "rank0_context_keys": n_ctx[-1]}
 
 
 def bench_stack(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
-    """One denoise step of all the Wan blocks of a preset (30 for 1.3B, 40 for 14B) over one 3-frame chunk
-    (4680 tokens, 30x52 grid) through the paged exchange at steady state: 8 store passes fill the clean list
-    (anchor + 7), and each timed step is chunk 8's forward (per layer the anchor re-RoPE + pack, the block
-    with its fused K/V pack, attention over anchor + 6 working chunks + self = 37440 keys in a 24-frame
-    window, 512-token text context)."""
+    """A steady-state wavefront tick of all the Wan blocks of a preset (30 for 1.3B, 40 for 14B) on one GPU:
+    rf_step 4, 21-frame window, 3-frame chunks of 4680 tokens (30x52 grid), 512-token text context.  8 store
+    passes through the stack fill the clean list (anchor + 7); the timed tick is tick 12: the store pass of
+    chunk 8 and the denoise passes of ranks 3..0 (chunks 9..12), each with its anchor re-RoPE and fused in-block
+    K/V pack.  Rank 0's pass -- one denoise step of one chunk -- attends over anchor + 2 working + live + self +
+    3 in-flight = 37440 keys and is also timed alone."""
+    from waveforcing_amd.exchange import TickPlan
     from waveforcing_amd.stack import QuantizedWanStack
 
     frames, h, w = 3, 30, 52
     st = QuantizedWanStack.random(preset, seed=100, device=dev, tokens_per_frame=h * w, frames_per_chunk=frames,
-                                  max_attn_frames=24)
+                                  max_attn_frames=21, rf_step=4)
+    ex = st.exchange
     dim = st.blocks[0].dim
     g = torch.Generator(device=dev).manual_seed(5)
     st.set_text(torch.randn((512, dim), generator=g, device=dev).to(torch.bfloat16))
     T = frames * h * w
     x0 = torch.randn((T, dim), generator=g, device=dev).to(torch.bfloat16)
     e = (torch.randn((frames, 6, dim), generator=g, device=dev) * 0.1).to(torch.bfloat16)
-    x = x0.clone()
+    xs = {k: x0.clone() for k in ("store", 0, 1, 2, 3)}
     for c in range(8):
-        x.copy_(x0)
-        st.forward_chunk(x, e, c, h, w, store=True)
-    n_ctx = st.exchange.layer_context(0, 8 * frames, frames, h, w)[3]
-    st.exchange.finish_denoise()
+        xs["store"].copy_(x0)
+        st.forward_chunk(xs["store"], e, c, h, w, store=True)
+    plan = TickPlan(STEADY_TICK, [0, 1, 2, 3], True, (STEADY_TICK - 3) * frames, 4 * frames)
+
+    def tick():
+        ex.begin_tick(plan)
+        try:
+            for key in ("store", 3, 2, 1, 0):
+                xs[key].copy_(x0)
+                p = ex.store_pass() if key == "store" else ex.denoise_pass(key)
+                st.run_pass(xs[key], e, p, h, w)
+        finally:
+            ex.abort_tick()   # the clean lists stay as they are: every timed tick is the same
+
+    ms_tick = _timed(tick, max(2, steps // 3), 1)
+    # rank 0's pass alone, inside an open tick whose other passes have run
+    ex.begin_tick(plan)
+    for key in ("store", 3, 2, 1):
+        p = ex.store_pass() if key == "store" else ex.denoise_pass(key)
+        st.run_pass(xs[key], e, p, h, w)
+    p0 = ex.denoise_pass(0)
+    n_ctx = ex.layer_context(0, p0, h, w)[3]
 
     def step():
-        x.copy_(x0)
-        st.forward_chunk(x, e, 8, h, w, store=False)
+        xs[0].copy_(x0)
+        st.run_pass(xs[0], e, p0, h, w)
 
     ms = _timed(step, steps, warmup)
+    ex.abort_tick()
     out = {"ms": ms, "ms_per_layer": ms / len(st.blocks), "layers": len(st.blocks), "tokens": T,
-           "context_keys": n_ctx, "tokens_per_s": T / (ms * 1e-3)}
-    del st, x, x0
+           "context_keys": n_ctx, "tokens_per_s": T / (ms * 1e-3), "ms_per_tick_5_passes": ms_tick}
+    del st, xs, x0
     torch.cuda.empty_cache()
     return out
 
@@ -325,6 +362,23 @@ def bench_copy(steps: int, warmup: int, dev: str):
     dst = torch.empty_like(src)
     ms = _timed(lambda: dst.copy_(src), steps, warmup)
     return {"ms": ms, "bytes_read": 1 << 30, "bytes_written": 1 << 30, "gbs": 2 * (1 << 30) / (ms * 1e-3) / 1e9}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (first ``model name`` line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+CPU_MODEL = _cpu_model()
 
 
 def cpu_baseline_kv() -> dict:
@@ -358,7 +412,7 @@ def cpu_baseline_kv() -> dict:
     return {
         "value": round(gbs, 3),
         "unit": "GB/s",
-        "cores": threads,
+        "cores": threads, "cpu_model": CPU_MODEL,
         "kind": "port",
         "sample": f"oracle torch-CPU pack of {n_layers} of the 30 layers (K and V), median of {len(reps)} reps",
     }
@@ -391,7 +445,7 @@ def cpu_baseline_extra() -> dict:
     ops = 2.0 * x.shape[0] * w.shape[0] * x.shape[1]
     t = _cpu_median(lambda: olin.i8_linear(x, w, b))
     out["w8a8_int8_linear"] = {"value": round(ops / t / 1e12, 4), "unit": "TOPS", "ms": round(t * 1e3, 2),
-                               "cores": threads, "kind": "port",
+                               "cores": threads, "cpu_model": CPU_MODEL, "kind": "port",
                                "sample": "oracle int8 linear 4680x1536x1536 incl. quantization (torch _int_mm)"}
     wq, ws = olin.fp8_quant_weight(w)
     rows = 64  # torch's CPU _scaled_mm is slow (~80 s for the whole 4680-row linear): a bounded sample
@@ -399,7 +453,7 @@ def cpu_baseline_extra() -> dict:
     ops_s = 2.0 * rows * w.shape[0] * x.shape[1]
     out["fp8_pertensor_linear"] = {"value": round(ops_s / t / 1e12, 6), "unit": "TFLOP/s",
                                    "ms_full_workload_extrapolated": round(t * x.shape[0] / rows * 1e3, 1),
-                                   "cores": threads, "kind": "port",
+                                   "cores": threads, "cpu_model": CPU_MODEL, "kind": "port",
                                    "sample": "oracle per-tensor e4m3 linear, 64 of the 4680 rows x 1536 x 1536 "
                                              "(torch _scaled_mm)"}
     g = torch.Generator().manual_seed(12)
@@ -410,7 +464,7 @@ def cpu_baseline_extra() -> dict:
     flops = 4.0 * lq * n_kv * HEAD_DIM
     full_ms = t * (TOKENS * HEADS) / lq * 1e3
     out["attention_8_chunks"] = {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s",
-                                 "ms_full_workload_extrapolated": round(full_ms, 1), "cores": threads, "kind": "port",
+                                 "ms_full_workload_extrapolated": round(full_ms, 1), "cores": threads, "cpu_model": CPU_MODEL, "kind": "port",
                                  "sample": "oracle SDPA, 256 queries x 1 head over 37440 keys, fp32; x 219.4 "
                                            "extrapolates to 4680 queries x 12 heads"}
     out["dit_block_1p3b"] = cpu_baseline_block(threads)
@@ -447,7 +501,7 @@ def cpu_baseline_block(threads: int) -> dict:
     t = _cpu_median(lambda: ob.block_forward(params, x, e, (frames, h, w), prior * frames, pk, pv, ctx, own,
                                              (prior + 1) * T, PAGE, tk, tv, heads), reps=3, budget_s=8.0)
     return {"value": round(t * 1e3, 1), "unit": "ms per block per 3-frame chunk", "higher_is_better": False,
-            "ms_30_layer_stack_extrapolated": round(30 * t * 1e3, 0), "cores": threads, "kind": "port",
+            "ms_30_layer_stack_extrapolated": round(30 * t * 1e3, 0), "cores": threads, "cpu_model": CPU_MODEL, "kind": "port",
             "sample": "oracle block_forward, whole 1.3B block: 4680 tokens over 37440 FP8 paged keys + 512 text "
                       "tokens (int8 _int_mm linears, fp32 SDPA)"}
 
@@ -560,19 +614,25 @@ def main() -> None:
             "attn_paged_fp8_context_sweep": {f"{c}_chunks": {"keys": r["keys"], "ms": round(r["ms"], 4),
                                                               "tflops": round(r["tflops"], 1)}
                                              for c, r in at_sweep.items()},
-            "exchange_1p3b_us_per_layer": round(xch["us_per_layer"], 2),
+            "exchange_1p3b_ms_per_tick": round(xch["ms_per_tick"], 4),
+            "exchange_1p3b_us_per_pass_layer": round(xch["us_per_pass_layer"], 2),
             "exchange_1p3b_gbs": round(xch["gbs"], 1),
-            "exchange_note": "denoise-side paged exchange per layer at steady state: this chunk's K/V packed into "
-                             "its slot + the anchor's K re-RoPEd and packed (65.4 MB algorithmic per layer); "
-                             "context anchor + 6 working + self = 37440 keys",
+            "exchange_note": "paged exchange of one steady-state tick (rf_step 4, 21-frame window): 5 passes x 30 "
+                             "layers of K/V packs into the passes' slots + 2 anchor re-RoPE packs over all layers "
+                             "(7.85 GB algorithmic); rank 0's context anchor + 2 working + live + self + 3 "
+                             "in-flight = 37440 keys",
             "dit_stack_1p3b_ms_per_chunk": round(stk["ms"], 3),
             "dit_stack_1p3b_ms_per_layer": round(stk["ms_per_layer"], 4),
             "dit_stack_1p3b_tokens_per_s": round(stk["tokens_per_s"], 1),
+            "dit_stack_1p3b_ms_per_tick_5_passes": round(stk["ms_per_tick_5_passes"], 3),
             "dit_stack_14b_ms_per_chunk": round(stk14["ms"], 2),
             "dit_stack_14b_ms_per_layer": round(stk14["ms_per_layer"], 3),
-            "dit_stack_note": "30 blocks of Wan-1.3B (40 of 14B) over one 4680-token chunk, one denoise step at steady state "
-                              "through the paged exchange (anchor re-RoPE + fused in-block K/V pack per layer, "
-                              "37440-key context), random init drawn on the GPU",
+            "dit_stack_14b_ms_per_tick_5_passes": round(stk14["ms_per_tick_5_passes"], 2),
+            "dit_stack_note": "30 blocks of Wan-1.3B (40 of 14B) over one 4680-token chunk: rank 0's denoise pass at a "
+                              "steady-state wavefront tick (rf_step 4, 21-frame window; context anchor + 2 working + "
+                              "live + self + 3 in-flight = 37440 keys, fused in-block K/V pack per layer), and the "
+                              "whole tick (store pass + 4 denoise passes, 2 anchor re-RoPEs); random init drawn on "
+                              "the GPU",
             "dit_block_1p3b_ms_per_chunk": round(b13["ms"], 4),
             "dit_block_14b_ms_per_chunk": round(b14["ms"], 4),
             "dit_block_note": "one block, 4680-token 3-frame chunk, 37440-key FP8 paged self-attn context, "

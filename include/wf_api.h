@@ -103,6 +103,23 @@ int wf_fp8_kv_pack_rope(const void* k, const void* v, int64_t n_tokens,
                         uint8_t* v_codes, float* k_scales, float* v_scales,
                         int64_t pool_pages, void* stream);
 
+/* wf_fp8_kv_pack_rope with a tiled table: token t is rotated by row
+ * t % rope_rows of cos/sin ([rope_rows][head_dim / 2] fp32), 1 <= rope_rows
+ * <= n_tokens.  One launch re-RoPEs a batch of equal chunks, e.g. the anchor
+ * of every layer (K [n_layers * T][H][D] with rope_rows = T and a page table
+ * over every layer's anchor pages in one pool): the per-layer
+ * _anchor_working rotation + slot copy (wave_rt/denoiser/exchange/
+ * common.py:70-91, paged.py:215-227), which uses the same table for every
+ * layer of a step, for all layers at once. */
+int wf_fp8_kv_pack_rope_tiled(const void* k, const void* v, int64_t n_tokens,
+                              int32_t n_heads, int32_t head_dim, int64_t ld_kv,
+                              const float* cos, const float* sin,
+                              int64_t rope_rows, const int32_t* page_table,
+                              int64_t n_table, int32_t page_tokens,
+                              uint8_t* k_codes, uint8_t* v_codes,
+                              float* k_scales, float* v_scales,
+                              int64_t pool_pages, void* stream);
+
 /* K straight from the fused QKV output into the pages: per token,
  * y = bf16(bf16(k * rsqrt(mean(k^2) + eps)) * norm_w) over the full row of
  * n_heads * head_dim values (as wf_rmsnorm_rope), stored to ku_out (bf16,

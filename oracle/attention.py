@@ -23,12 +23,19 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None 
     """q [Lq, H, D], k/v [Lk, H, D] -> fp32 [Lq, H, D]; softmax(q k^T * scale) v per head."""
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
-    qh = q.float().transpose(0, 1)  # [H, Lq, D]
-    kh = k.float().transpose(0, 1)
-    vh = v.float().transpose(0, 1)
-    s = torch.matmul(qh, kh.transpose(1, 2)) * scale
-    pr = torch.softmax(s, dim=-1)
-    return torch.matmul(pr, vh).transpose(0, 1)
+    H = q.shape[1]
+    # the score tensor of a whole 14B context is tens of GB: heads go in groups of at most 2^28 scores
+    group = max(1, min(H, (1 << 28) // max(1, q.shape[0] * k.shape[0])))
+    outs = []
+    for h0 in range(0, H, group):
+        sl = slice(h0, h0 + group)
+        qh = q[:, sl].float().transpose(0, 1)  # [h, Lq, D]
+        kh = k[:, sl].float().transpose(0, 1)
+        vh = v[:, sl].float().transpose(0, 1)
+        s = torch.matmul(qh, kh.transpose(1, 2)) * scale
+        pr = torch.softmax(s, dim=-1)
+        outs.append(torch.matmul(pr, vh).transpose(0, 1))
+    return outs[0] if len(outs) == 1 else torch.cat(outs, dim=1)
 
 
 def paged_fp8(q, k_pool, v_pool, table: Sequence[int], n_kv: int, page_tokens: int, scale=None) -> torch.Tensor:

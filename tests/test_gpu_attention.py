@@ -16,7 +16,7 @@ import torch
 from oracle import attention as oat
 from oracle import kv as okv
 from waveforcing_amd import inputs
-from waveforcing_amd.backend import _WAVE_STATE, attend, attn_paged_fp8, enable_hip_fp8
+from waveforcing_amd.backend import _WAVE_STATE, attend, attn_dense_bf16, attn_paged_fp8, enable_hip_fp8
 from waveforcing_amd.kv import Fp8PagePool, PagedKV
 
 pytestmark = pytest.mark.gpu
@@ -87,6 +87,33 @@ def test_full_context_sampled_rows():
     ref = oat.paged_fp8(q[rows], kp, vp, ids, n_kv, page)
     err = (out[rows].float() - ref).abs().max().item()
     print(f"max abs err {err:.3e}")
+    assert err <= TOL, err
+
+
+def test_full_context_14b_heads_sampled_rows():
+    """The 14B geometry: 4680 queries x 40 heads over 8 chunks (37440 keys); 160 sampled rows, all heads."""
+    Lq, H, n_kv, page = 4680, 40, 37440, 1560
+    q, pool, ctx, ids, kp, vp, _ = _setup(Lq, H, n_kv, page, 26, seed=50)
+    out = attn_paged_fp8(q.to(DEV), ctx).cpu()
+    rows = torch.cat([torch.arange(0, 64), torch.arange(Lq - 32, Lq),
+                      torch.randperm(Lq, generator=torch.Generator().manual_seed(6))[:64]])
+    ref = oat.paged_fp8(q[rows], kp, vp, ids, n_kv, page)
+    err = (out[rows].float() - ref).abs().max().item()
+    print(f"max abs err {err:.3e}")
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("H", [12, 40])
+def test_dense_cross_attention_full_size(H):
+    """The text cross-attention: 4680 queries over 512 dense bf16 text keys (wf_attn_dense_bf16), all rows."""
+    g = torch.Generator().manual_seed(60 + H)
+    q = torch.randn((4680, H, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((512, H, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((512, H, 128), generator=g).to(torch.bfloat16)
+    out = attn_dense_bf16(q.to(DEV), k.to(DEV), v.to(DEV)).cpu().float()
+    ref = oat.sdpa(q, k, v)
+    err = (out - ref).abs().max().item()
+    print(f"H={H}: max abs err {err:.3e}")
     assert err <= TOL, err
 
 

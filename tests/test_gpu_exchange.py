@@ -1,89 +1,135 @@
-"""GPU parity of the single-GPU paged exchange over several chunks.
+"""GPU parity of the single-GPU paged exchange over a whole wavefront.
 
-A plain list model of the reference's clean list and context assembly
-(wave_rt/denoiser/exchange/common.py:70-114, paged.py:156-310), holding bf16
-tensors as the reference does, builds each step's context as anchor
-(re-RoPEd by the oracle's table rotation at ``csf - wflen - npb``) + working
-set + self.  The oracle's per-(token, head) quantize/dequantize of that
-context must equal, bit for bit, the dequantized pages the exchange hands to
-attention.  The store passes promote chunks 0..9, so the clean list wraps
-(anchor + last 7) and slots are recycled.
+Ticks 0..14 of an 11-chunk stream at rf_step 4 with a 21-frame window
+(wave_rt/denoiser/engine.py:300-420): every pass of every tick calls its
+exchange closure through the patched-forward route of
+wave_rt/runtime/backend.py:87-157 -- ``set_exchange_fn(closure)``, then
+``exchange_and_attend`` with the ``hip_fp8`` backend and profiling on.
+
+A plain list model of the reference's contexts, holding bf16 tensors as the
+reference does, builds each pass's K/V: store [anchor, working..., self]
+(common.py:93-107), denoise [anchor, working..., live, self, in-flight
+n > r ...] (paged.py:161-190), the anchor re-RoPEd by the oracle's table
+rotation at ``csf - wflen - npb``.  Checked for every (pass, layer):
+
+* the oracle's per-(token, head) quantize/dequantize of that context equals,
+  bit for bit, the dequantized pages the closure hands to attention;
+* the attention output equals the oracle's fp32 SDPA over that context within
+  2e-2 max-abs;
+* ``prof_read()`` reports the context length as ``klen`` and positive
+  exchange and attention times.
+
+The steady-state denoise context of rank 0 is 8 chunks: anchor + 2 working
++ live + self + 3 in-flight.
 """
 
 import pytest
 import torch
 
+from oracle import attention as oat
 from oracle import block as ob
 from oracle import kv as okv
+from waveforcing_amd import backend
 from waveforcing_amd import exchange as ex
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 NPB, HT, WD, H = 3, 8, 8, 2          # 3-frame chunks of 8 x 8 tokens per frame, 2 heads
 T = NPB * HT * WD
-WINDOW = 18                          # 18-frame attention window: 4 working chunks for one query chunk
+WINDOW, RF, N_CHUNKS, LAYERS = 21, 4, 11, 2
 
 
-def _chunk(seed):
-    g = torch.Generator().manual_seed(seed)
+def _kv(t, rank, layer):
+    g = torch.Generator().manual_seed(100000 + 1000 * t + 10 * rank + layer)
     mk = lambda: (torch.randn((1, T, H, 128), generator=g) * 2).to(torch.bfloat16)
-    return mk(), mk(), mk()          # roped K, un-rotated K, V
+    return mk(), mk(), mk(), mk()          # q, roped K, un-rotated K, V
 
 
-def _oracle_context(model, csf, qf, kr, v):
-    """model: list of dicts(kr, ku, v) (anchor first) -> dequantized K, V of the context."""
+def _model_context(clean, live, inflight, plan, rank, layer):
+    """Dequantized K, V of the list model's context for a pass (rank RF = store)."""
+    if rank == RF:
+        csf, qf = (plan.tick - RF) * NPB, NPB
+    else:
+        csf, qf = plan.csf, plan.qf
     ks, vs = [], []
-    if model:
-        n_a, n_w = ex.anchor_and_working(len(model), ex.working_chunks(WINDOW, qf, NPB))
-        working = model[len(model) - n_w:] if n_w else []
-        start = csf - len(working) * NPB - NPB
-        ang = ob.rope_angles(NPB, HT, WD, start)
-        ak = ob.rope_apply_table(model[0]["ku"][0], torch.cos(ang).float(), torch.sin(ang).float())
-        ks += [ak] + [w["kr"][0] for w in working]
-        vs += [model[0]["v"][0]] + [w["v"][0] for w in working]
-    ks.append(kr[0])
-    vs.append(v[0])
+    if clean:
+        _, n_w = ex.anchor_and_working(len(clean), ex.working_chunks(WINDOW, qf, NPB))
+        working = clean[len(clean) - n_w:] if n_w else []
+        ang = ob.rope_angles(NPB, HT, WD, ex.anchor_rope_start(csf, len(working), NPB))
+        ks.append(ob.rope_apply_table(clean[0]["ku"][layer][0], torch.cos(ang).float(), torch.sin(ang).float()))
+        vs.append(clean[0]["v"][layer][0])
+        ks += [w["kr"][layer][0] for w in working]
+        vs += [w["v"][layer][0] for w in working]
+    if rank == RF:
+        chunks = [live]
+    else:
+        chunks = ([live] if plan.store_active else []) + [inflight[n] for n in ex.inflight_order(rank, plan.act_ranks)]
+    ks += [c["kr"][layer][0] for c in chunks]
+    vs += [c["v"][layer][0] for c in chunks]
     rt = lambda x: okv.dequantize_rows(*okv.quantize_rows(x))
     return rt(torch.cat(ks, 0)), rt(torch.cat(vs, 0))
 
 
-def _check(ctx_pair, want):
-    ctx, ctx_v = ctx_pair
-    assert ctx_v is ctx
-    k, v = ctx.pool.unpack(ctx.table, ctx.n_tokens)
-    assert ctx.shape == (1, want[0].shape[0], H, 128)
-    assert torch.equal(k.cpu(), want[0]) and torch.equal(v.cpu(), want[1])
+def test_wavefront_contexts_and_patched_attention_match_list_model():
+    x = ex.PagedExchange(n_layers=LAYERS, n_heads=H, tokens_per_frame=HT * WD, frames_per_chunk=NPB,
+                         max_attn_frames=WINDOW, rf_step=RF, device=DEV)
+    backend.enable_hip_fp8()
+    clean = []
+    longest = 0
+    try:
+        for t in range(N_CHUNKS + RF):
+            plan = x.begin_tick_at(t, N_CHUNKS)
+            live, inflight = None, {}
+            order = ([RF] if plan.store_active else []) + sorted(plan.act_ranks, reverse=True)
+            for rank in order:
+                closure = x.make_store_exch() if rank == RF else x.make_denoise_exch(rank)
+                seen = []
 
+                def recording(**kw):
+                    seen.append(closure(**kw))
+                    return seen[-1]
 
-def _call(exch, layer, kr, ku, v):
-    return exch(layer_idx=layer, roped_query=None, roped_key=kr.to(DEV), unroped_key=ku.to(DEV), value=v.to(DEV),
-                current_start=0, tokens_per_frame=HT * WD, post_patch_height=HT, post_patch_width=WD, dim=H * 128,
-                rope_num_heads=H, num_frames_per_block=NPB)
-
-
-def test_store_and_denoise_contexts_match_list_model():
-    L = 2
-    x = ex.PagedExchange(n_layers=L, n_heads=H, tokens_per_frame=HT * WD, frames_per_chunk=NPB,
-                         max_attn_frames=WINDOW, device=DEV)
-    model = [[] for _ in range(L)]
-    for c in range(10):
-        # denoise step for chunk c + 1 against the clean list of chunks < c
-        exch = x.make_denoise_exch((c + 1) * NPB)
-        for layer in range(L):
-            kr, ku, v = _chunk(1000 * c + 10 * layer + 1)
-            _check(_call(exch, layer, kr, ku, v), _oracle_context(model[layer], (c + 1) * NPB, NPB, kr, v))
-        x.finish_denoise()
-        # store pass for chunk c, then promotion into the clean list
-        store_kv = {}
-        exch = x.make_store_exch(c, store_kv)
-        for layer in range(L):
-            kr, ku, v = _chunk(1000 * c + 10 * layer)
-            _check(_call(exch, layer, kr, ku, v), _oracle_context(model[layer], c * NPB, NPB, kr, v))
-            page = dict(kr=kr, ku=ku, v=v)
-            model[layer].append(page)
-            if len(model[layer]) > 8:
-                model[layer][:] = model[layer][:1] + model[layer][-7:]
-        x.promote(store_kv, cid=c)
-        for layer in range(L):
-            assert len(x.clean[layer]) == len(model[layer])
+                backend.set_exchange_fn(recording)
+                entry = {"kr": [], "ku": [], "v": []}
+                for layer in range(LAYERS):
+                    q, kr, ku, v = _kv(t, rank, layer)
+                    entry["kr"].append(kr)
+                    entry["ku"].append(ku)
+                    entry["v"].append(v)
+                    if rank == RF:
+                        live = entry
+                    else:
+                        inflight[rank] = entry
+                    backend.prof_reset(True)
+                    out = backend.exchange_and_attend(layer, q.to(DEV), kr.to(DEV), ku.to(DEV), v.to(DEV),
+                                                      current_start=(t - rank) * NPB * HT * WD,
+                                                      tokens_per_frame=HT * WD, post_patch_height=HT,
+                                                      post_patch_width=WD, dim=H * 128, rope_num_heads=H,
+                                                      num_frames_per_block=NPB)
+                    attn_ms, exch_ms, klen = backend.prof_read()
+                    ctx, ctx_v = seen[-1]
+                    assert ctx_v is ctx
+                    wk, wv = _model_context(clean, live, inflight, plan, rank, layer)
+                    k, vv = ctx.pool.unpack(ctx.table, ctx.n_tokens)
+                    assert ctx.shape == (1, wk.shape[0], H, 128) and klen == wk.shape[0]
+                    assert torch.equal(k.cpu(), wk) and torch.equal(vv.cpu(), wv), f"tick {t} rank {rank} L{layer}"
+                    assert attn_ms > 0 and exch_ms > 0
+                    ref = oat.sdpa(q[0], wk, wv)
+                    err = (out[0].cpu().float() - ref).abs().max().item()
+                    assert out.shape == q.shape and err <= 2e-2, f"tick {t} rank {rank} L{layer}: {err:.3e}"
+                    longest = max(longest, wk.shape[0])
+            backend.set_exchange_fn(None)
+            x.end_tick()
+            if plan.store_active:
+                clean.append(live)
+                if len(clean) > 8:
+                    clean[:] = clean[:1] + clean[-7:]
+            for layer in range(LAYERS):
+                assert len(x.clean[layer]) == len(clean)
+    finally:
+        backend.set_exchange_fn(None)
+        backend.prof_reset(False)
+        backend._WAVE_STATE["attn"] = "torch_sdpa"
+        backend._WAVE_STATE["fa_func"] = None
     torch.cuda.synchronize()
+    assert longest == 8 * T     # anchor + 2 working + live + self + 3 in-flight

@@ -1,17 +1,22 @@
-"""GPU parity of the block stack driven through the paged exchange.
+"""GPU parity of the block stack driven tick by tick through the paged exchange.
 
-* Replay: a stack of 2 layers runs a denoise step and a store pass for each
-  of chunks 0..9 (the clean list grows past the working set, then wraps at
-  anchor + last 7, and slots are recycled).  A hand-written replay with the
-  same blocks, a pool of its own (one fixed page range per chunk, no
-  recycling) and a list model of the clean list (anchor re-RoPEd to
-  ``csf - wflen - npb``, working set, chunk: common.py:70-114) must give the
-  same hidden states, bit for bit, at every step.
-* Oracle: stores of chunks 0..3 and a denoise step of chunk 4, which
-  re-RoPEs the anchor to frame 3, against the CPU block oracle chained over
-  the layers with its own pools and clean list.  Bar as for one block
-  (relative L2 <= 1e-2, max |diff| <= 5e-2 * max |x|), since every input x
-  is fresh and only the context carries differences between the two sides.
+The wavefront's schedule (wave_rt/denoiser/engine.py:300-420) at rf_step 2:
+each tick runs the store rank's pass and the active denoise ranks' passes.
+
+* Replay: ticks 0..10 of a 9-chunk stream through a 2-layer stack (the clean
+  list grows past the working set and wraps at anchor + last 7, slots are
+  recycled).  A hand-written replay with the same blocks, a pool of its own
+  (one fixed page range per chunk, no recycling) and a list model of the
+  reference's contexts (store: anchor + working + self; denoise: anchor +
+  working + live + self + in-flight n > r, paged.py:161-190, with the anchor
+  re-RoPEd to ``csf - wflen - npb``, common.py:70-91) must give the same
+  hidden states, bit for bit, for every pass.
+* Oracle: ticks 0..5 of a 4-chunk stream against the CPU block oracle
+  chained over the layers with its own pools and the same list model
+  (anchor re-RoPE included).  Bar as for one block (relative L2 <= 1e-2,
+  max |diff| <= 5e-2 * max |x|), since every input x is fresh and only the
+  context carries differences between the two sides.
+* A failing layer returns every slot of the tick and promotes nothing.
 """
 
 import pytest
@@ -31,7 +36,8 @@ DIM, HEADS, FFN = 256, 2, 512
 NPB, HT, WD = 3, 8, 8              # 64-token pages: the attention kernel's key tile
 PAGE = HT * WD
 T = NPB * PAGE
-WINDOW = 12        # (12 - 3 - 3) // 3 = 2 working chunks
+WINDOW = 15        # one query chunk: (15 - 3 - 3) // 3 = 3 working chunks; two (rf_step 2): 2
+RF = 2
 LAYERS = 2
 
 
@@ -39,8 +45,9 @@ def _params():
     return [random_block_params(DIM, FFN, seed=70 + i) for i in range(LAYERS)]
 
 
-def _inputs(c, store):
-    g = torch.Generator().manual_seed(1000 + 2 * c + int(store))
+def _inputs(t, rank):
+    """Seeded hidden states and modulation of a pass (rank RF = the store rank)."""
+    g = torch.Generator().manual_seed(1000 + 10 * t + rank)
     x = torch.randn((T, DIM), generator=g).to(torch.bfloat16)
     e = (torch.randn((NPB, 6, DIM), generator=g) * 0.1).to(torch.bfloat16)
     return x, e
@@ -52,120 +59,129 @@ def _text():
 
 def _stack(params):
     blocks = [QuantizedWanBlock(p, HEADS, DEV) for p in params]
-    xch = ex.PagedExchange(LAYERS, HEADS, PAGE, NPB, WINDOW, device=DEV)
+    xch = ex.PagedExchange(LAYERS, HEADS, PAGE, NPB, WINDOW, rf_step=RF, device=DEV)
     st = QuantizedWanStack(blocks, xch)
     st.set_text(_text().to(DEV))
     return st
-
-
-def _list_context(clean, csf, qf=NPB):
-    """(anchor cid or None, anchor rope start, working cids) of the clean list model."""
-    if not clean:
-        return None, None, []
-    _, n_w = ex.anchor_and_working(len(clean), ex.working_chunks(WINDOW, qf, NPB))
-    working = clean[len(clean) - n_w:] if n_w else []
-    return clean[0], ex.anchor_rope_start(csf, len(working), NPB), working
-
-
-def _keep_last(clean):
-    return clean[:1] + clean[-7:] if len(clean) > 8 else clean
 
 
 def _pages(c):
     return list(range(NPB * c, NPB * c + NPB))
 
 
-@pytest.mark.parametrize("qf", [NPB, 2 * NPB])   # one query chunk (2 working chunks) or two (1)
-def test_stack_equals_manual_replay_over_ten_chunks(qf):
+def _passes(plan):
+    """(rank, chunk, csf, qf) of a tick's passes in execution order; rank RF is the store rank."""
+    out = [(RF, plan.tick - RF, (plan.tick - RF) * NPB, NPB)] if plan.store_active else []
+    return out + [(r, plan.tick - r, plan.csf, plan.qf) for r in sorted(plan.act_ranks, reverse=True)]
+
+
+def _context(clean, plan, rank, csf, qf):
+    """List model: (anchor chunk or None, its rope start, context chunk ids in the reference's order)."""
+    anchor, start, ids = None, None, []
+    if clean:
+        _, n_w = ex.anchor_and_working(len(clean), ex.working_chunks(WINDOW, qf, NPB))
+        working = clean[len(clean) - n_w:] if n_w else []
+        anchor, start = clean[0], ex.anchor_rope_start(csf, len(working), NPB)
+        ids = [anchor] + working
+    if rank == RF:
+        return anchor, start, ids + [plan.tick - RF]
+    if plan.store_active:
+        ids.append(plan.tick - RF)
+    return anchor, start, ids + [plan.tick - n for n in ex.inflight_order(rank, plan.act_ranks)]
+
+
+def _keep_last(clean):
+    return clean[:1] + clean[-7:] if len(clean) > 8 else clean
+
+
+def test_stack_ticks_equal_manual_replay():
     params = _params()
     st = _stack(params)
     blocks = st.blocks
-    n_chunks = 10
-    own_pages = _pages(n_chunks)                      # the denoise step's own pages
-    pools = [Fp8PagePool(NPB * (n_chunks + 1), HEADS, 128, PAGE, DEV) for _ in range(LAYERS)]
+    n_chunks = 9
+    pools = [Fp8PagePool(NPB * n_chunks, HEADS, 128, PAGE, DEV) for _ in range(LAYERS)]
     text = [b.text_kv(_text().to(DEV)) for b in blocks]
-    clean = [[] for _ in range(LAYERS)]
-    anchor_ku = [None] * LAYERS
-    for c in range(n_chunks):
-        csf = c * NPB
-        cos, sin = rope.cos_sin(NPB, HT, WD, csf, device=DEV)
-        for store in (False, True):
-            x, e = _inputs(c, store)
-            q = NPB if store else qf     # store passes carry one chunk (paged.py:257-310)
-            got = st.forward_chunk(x.to(DEV).clone(), e.to(DEV), c, HT, WD, store=store, query_frames=q)
+    clean, anchor_ku = [], [None] * LAYERS
+    for t in range(n_chunks + RF):
+        plan = ex.tick_plan(t, RF, n_chunks, NPB)
+        ins = {(r if r != RF else "store"): _inputs(t, r) for r, *_ in _passes(plan)}
+        got = {k: (x.to(DEV).clone(), e.to(DEV)) for k, (x, e) in ins.items()}
+        st.tick(plan, got, HT, WD)
+        for r, c, csf, qf in _passes(plan):
+            x, e = ins["store" if r == RF else r]
             want = x.to(DEV).clone()
+            cos, sin = rope.cos_sin(NPB, HT, WD, c * NPB, device=DEV)
+            anchor, start, ids = _context(clean, plan, r, csf, qf)
             for L, blk in enumerate(blocks):
                 pool = pools[L]
-                anchor, start, working = _list_context(clean[L], csf, q)
-                ctx_pages = []
                 if anchor is not None:
                     acos, asin = rope.cos_sin(NPB, HT, WD, start, device=DEV)
                     pool.pack(anchor_ku[L], None, pool.page_table(_pages(anchor)), rope=(acos, asin))
-                    ctx_pages = _pages(anchor) + [p for w in working for p in _pages(w)]
-                own = _pages(c) if store else own_pages
-                ku = torch.empty_like(want) if store and not clean[L] else None
-                blk.forward(want, e.to(DEV), cos, sin, pool, pool.page_table(ctx_pages + own), pool.page_table(own),
-                            len(ctx_pages) * PAGE + T, text[L], unroped_k_out=ku)
-                if store:
-                    if ku is not None:
-                        anchor_ku[L] = ku.view(T, HEADS, 128).clone()
-                    clean[L] = _keep_last(clean[L] + [c])
-            assert torch.equal(got, want), f"chunk {c} store={store}"
-        assert [[p.cid for p in lst] for lst in st.exchange.clean] == clean
+                ku = torch.empty_like(want) if r == RF and not clean else None
+                blk.forward(want, e.to(DEV), cos, sin, pool, pool.page_table([p for i in ids for p in _pages(i)]),
+                            pool.page_table(_pages(c)), len(ids) * T, text[L], unroped_k_out=ku)
+                if ku is not None:
+                    anchor_ku[L] = ku.view(T, HEADS, 128).clone()
+            assert torch.equal(got["store" if r == RF else r][0], want), f"tick {t} rank {r}"
+        if plan.store_active:
+            clean = _keep_last(clean + [t - RF])
+        assert [[p.cid for p in lst] for lst in st.exchange.clean] == [clean] * LAYERS
     # every slot is back on a free list or in a clean list
     for L in range(LAYERS):
         held = sorted(st.exchange._free[L] + [p.slot for p in st.exchange.clean[L]])
         assert held == list(range(st.exchange.n_slots))
 
 
-def test_stack_matches_oracle_chain_with_anchor_rerope():
+def test_stack_ticks_match_oracle_chain_with_anchor_rerope():
     params = _params()
     st = _stack(params)
     ctx_text = _text()
     otext = [ob.text_kv(p, ctx_text, HEADS) for p in params]
-    P = NPB * 6
-    own_pages = _pages(5)
-    pk = [okv.new_pool(P, PAGE, HEADS, 128) for _ in range(LAYERS)]
-    pv = [okv.new_pool(P, PAGE, HEADS, 128) for _ in range(LAYERS)]
-    clean = [[] for _ in range(LAYERS)]
-    anchor_ku = [None] * LAYERS
-    steps = [(c, True) for c in range(4)] + [(4, False)]
-    for c, store in steps:
-        x, e = _inputs(c, store)
-        got = st.forward_chunk(x.to(DEV).clone(), e.to(DEV), c, HT, WD, store=store).cpu().double()
-        ref = x
-        csf = c * NPB
-        for L, p in enumerate(params):
-            anchor, start, working = _list_context(clean[L], csf)
-            ctx_pages = []
-            if anchor is not None:
-                ang = ob.rope_angles(NPB, HT, WD, start)
-                ak = ob.rope_apply_table(anchor_ku[L], torch.cos(ang).float(), torch.sin(ang).float())
-                okv.pack(ak, _pages(anchor), PAGE, *pk[L])
-                ctx_pages = _pages(anchor) + [q for w in working for q in _pages(w)]
-            own = _pages(c) if store else own_pages
-            ref, ku = ob.block_forward(p, ref, e, (NPB, HT, WD), csf, pk[L], pv[L], ctx_pages + own, own,
-                                       len(ctx_pages) * PAGE + T, PAGE, *otext[L], HEADS, return_unroped_k=True)
-            if store:
-                if not clean[L]:
+    n_chunks = 4
+    pk = [okv.new_pool(NPB * n_chunks, PAGE, HEADS, 128) for _ in range(LAYERS)]
+    pv = [okv.new_pool(NPB * n_chunks, PAGE, HEADS, 128) for _ in range(LAYERS)]
+    clean, anchor_ku = [], [None] * LAYERS
+    moved = False
+    for t in range(n_chunks + RF):
+        plan = ex.tick_plan(t, RF, n_chunks, NPB)
+        ins = {(r if r != RF else "store"): _inputs(t, r) for r, *_ in _passes(plan)}
+        got = {k: (x.to(DEV).clone(), e.to(DEV)) for k, (x, e) in ins.items()}
+        st.tick(plan, got, HT, WD)
+        for r, c, csf, qf in _passes(plan):
+            x, e = ins["store" if r == RF else r]
+            ref = x
+            anchor, start, ids = _context(clean, plan, r, csf, qf)
+            moved |= anchor is not None and start != anchor * NPB
+            for L, p in enumerate(params):
+                if anchor is not None:
+                    ang = ob.rope_angles(NPB, HT, WD, start)
+                    ak = ob.rope_apply_table(anchor_ku[L], torch.cos(ang).float(), torch.sin(ang).float())
+                    okv.pack(ak, _pages(anchor), PAGE, *pk[L])
+                ref, ku = ob.block_forward(p, ref, e, (NPB, HT, WD), c * NPB, pk[L], pv[L],
+                                           [q for i in ids for q in _pages(i)], _pages(c), len(ids) * T, PAGE,
+                                           *otext[L], HEADS, return_unroped_k=True)
+                if r == RF and not clean:
                     anchor_ku[L] = ku
-                clean[L] = _keep_last(clean[L] + [c])
-        if c == 4:
-            assert _list_context(clean[0], csf)[1] == 3   # the anchor really moved
-        ref = ref.double()
-        rel = ((got - ref).norm() / ref.norm()).item()
-        mx = (got - ref).abs().max().item()
-        print(f"chunk {c} store={store}: rel L2 {rel:.3e}, max abs {mx:.3e}, max|x| {ref.abs().max().item():.2f}")
-        assert rel <= 1e-2
-        assert mx <= 5e-2 * ref.abs().max().item()
+            out = got["store" if r == RF else r][0].cpu().double()
+            ref = ref.double()
+            rel = ((out - ref).norm() / ref.norm()).item()
+            mx = (out - ref).abs().max().item()
+            print(f"tick {t} rank {r} chunk {c}: {len(ids)} context chunks, rel L2 {rel:.3e}, max abs {mx:.3e}")
+            assert rel <= 1e-2
+            assert mx <= 5e-2 * ref.abs().max().item()
+        if plan.store_active:
+            clean = _keep_last(clean + [t - RF])
+    assert moved   # some pass rotated the anchor away from its own position
 
 
-def test_stack_releases_slots_when_a_layer_fails():
+def test_stack_tick_releases_slots_when_a_layer_fails():
     st = _stack(_params())
-    x, _ = _inputs(0, True)
+    x, _ = _inputs(0, 0)
     e5 = torch.zeros((5, 6, DIM), dtype=torch.bfloat16, device=DEV)   # 192 tokens do not split into 5 frames
+    plan = ex.tick_plan(RF, RF, 4, NPB)                                 # store pass + ranks 0 and 1
+    ins = {k: (x.to(DEV).clone(), e5) for k in ("store", 0, 1)}
     with pytest.raises(ValueError, match="5 frames"):
-        st.forward_chunk(x.to(DEV), e5, 0, HT, WD, store=True)
+        st.tick(plan, ins, HT, WD)
     assert all(len(f) == st.exchange.n_slots for f in st.exchange._free) and not any(st.exchange.clean)
     with pytest.raises(ValueError, match="5 frames"):
         st.forward_chunk(x.to(DEV), e5, 0, HT, WD, store=False)

@@ -72,6 +72,36 @@ def test_gemm_exact(M, N, K):
     assert torch.equal(y, oy)
 
 
+@pytest.mark.parametrize("N,K,gelu", [
+    (15360, 5120, False),   # 14B fused QKV
+    (5120, 5120, False),    # 14B O
+    (13824, 5120, True),    # 14B fc_in + GELU
+    (5120, 13824, False),   # 14B fc_out
+])
+def test_gemm_14b_shapes_sampled_rows(N, K, gelu):
+    """The 14B block's linears on a 4680-token chunk; int32 accumulators exact and bf16 outputs exact (GELU:
+    within the stated tolerance) on 288 rows: the first two and the last tile rows, and random rows."""
+    M = 4680
+    seed = N + K
+    x = inputs.outlier_activations(M, K, seed=seed, chan_seed=seed + 1)
+    w, b = inputs.linear_weights(N, K, w_seed=seed + 2, b_seed=seed + 3)
+    qx, sx = olin.i8_quant_rows(x)
+    qw, sw = olin.i8_quant_rows(w)
+    del x, w
+    acc = torch.empty((M, N), dtype=torch.int32, device=DEV)
+    y = gemm_i8(qx.to(DEV), qw.to(DEV), sx.to(DEV), sw.to(DEV), b.to(DEV), gelu=gelu, acc_out=acc).cpu()
+    rows = torch.cat([torch.arange(0, 256, 8), torch.arange(M - 128, M),
+                      torch.randperm(M, generator=torch.Generator().manual_seed(seed))[:128]])
+    acc = acc.cpu()[rows]
+    oy, oacc = olin.i8_gemm(qx[rows].contiguous(), qw, sx[rows].contiguous(), sw, b, gelu=gelu)
+    assert torch.equal(acc, oacc)
+    if gelu:
+        rel = (y[rows].float() - oy.float()).norm() / oy.float().norm()
+        assert rel < 1e-2, float(rel)
+    else:
+        assert torch.equal(y[rows], oy)
+
+
 def test_gemm_no_bias_exact():
     y, acc, oy, oacc = _gemm_case(700, 384, 512, seed=3, bias=False)
     assert torch.equal(acc, oacc) and torch.equal(y, oy)

@@ -11,14 +11,23 @@
   agrees with the float64 complex rotation to one bf16 ulp and exactly in
   all but a few near-tie elements, is exact for the rotations by 0, 90 and
   180 degrees, and equals a scalar numpy-float32 evaluation element by
-  element.
+  element;
+- the wiring of causal_model.py:376-398 (which modulation chunk is which
+  shift, scale and gate, which norm feeds which branch, the order of the
+  three residuals) equals the closed forms of tests/block_probes.py exactly;
+  every swap of two modulation chunks and every other residual order changes
+  at least one probe's output.
 """
 
 import dataclasses
+import itertools
+
+import pytest
 
 import numpy as np
 import torch
 
+import block_probes as bp
 from oracle import block as ob
 from oracle import kv as okv
 from waveforcing_amd import rope
@@ -119,3 +128,37 @@ def test_rope_table_form_equals_scalar_float32():
             ci, si = np.float32(c[t, i]), np.float32(s[t, i])
             assert got[t, 0, 2 * i] == bf16(np.float32(a * ci) - np.float32(b * si))
             assert got[t, 0, 2 * i + 1] == bf16(np.float32(a * si) + np.float32(b * ci))
+
+
+PROBES = ("residuals", "ffn_mod", "attn_mod", "cross")
+
+
+def _run_probe(params, pr, e=None):
+    pk, pv = bp.pools()
+    tk, tv = ob.text_kv(params, pr["text"], bp.HEADS)
+    return ob.block_forward(params, pr["x"], pr["e"] if e is None else e, (bp.FRAMES, bp.HT, bp.WD), 0, pk, pv,
+                            [0, 1, 2], [0, 1, 2], bp.T, bp.PAGE, tk, tv, bp.HEADS)
+
+
+@pytest.mark.parametrize("kind", PROBES)
+def test_block_wiring_equals_closed_form(kind):
+    pr = bp.build(kind)
+    assert torch.equal(_run_probe(pr["params"], pr), pr["expected"])
+    # another gate chunk or another residual order is visible in this probe
+    for alt in bp.alternatives(pr):
+        assert not torch.equal(alt, pr["expected"])
+
+
+def test_every_swap_of_two_modulation_chunks_is_caught():
+    """Chunks i and j of the modulation and of e exchanged before the call is what an oracle reading chunk j
+    where it should read i (and i for j) computes; some probe must see every such swap."""
+    caught = set()
+    for kind in PROBES:
+        pr = bp.build(kind)
+        for i, j in itertools.combinations(range(6), 2):
+            perm = list(range(6))
+            perm[i], perm[j] = j, i
+            p = dataclasses.replace(pr["params"], modulation=pr["params"].modulation[:, perm])
+            if not torch.equal(_run_probe(p, pr, e=pr["e"][:, perm]), pr["expected"]):
+                caught.add((i, j))
+    assert caught == set(itertools.combinations(range(6), 2))

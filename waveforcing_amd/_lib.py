@@ -40,6 +40,13 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
         _c_void_p,
     ],
+    "wf_fp8_kv_pack_rope_tiled": [
+        _c_void_p, _c_void_p, _i64, _i32, _i32, _i64,
+        _c_void_p, _c_void_p, _i64,
+        _c_void_p, _i64, _i32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+        _c_void_p,
+    ],
     "wf_k_norm_rope_kv_pack": [
         _c_void_p, _c_void_p, _i64, _i32, _i32, _i64,
         _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,

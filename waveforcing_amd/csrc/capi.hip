@@ -88,7 +88,7 @@ extern "C" {
 
 const char* wf_last_error(void) { return wf::error_buffer(); }
 
-int wf_abi_version(void) { return (1 << 16) | 0; }
+int wf_abi_version(void) { return (1 << 16) | 1; }
 
 int wf_fp8_e4m3_encode_f32(const float* x, uint8_t* codes, int64_t n, void* stream) {
   WF_REQUIRE(n >= 0, WF_E_INVALID, "wf_fp8_e4m3_encode_f32: n=%lld < 0", (long long)n);

@@ -171,13 +171,15 @@ __device__ inline void st16(uint4* p, const uint4& v) {
   }
 }
 
-// ROPE: K rows are rotated by the token's row of cos/sin [n_tokens][64] first.
+// ROPE: K rows are rotated first, token t by row t % rope_rows of cos/sin
+// [rope_rows][64] (rope_rows = n_tokens: one row per token; a chunk's
+// token count: one table for a batch of equal chunks).
 template <bool NT_LOAD, bool NT_STORE, bool ROPE>
 __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ k, const uint4* __restrict__ v,
                                                       int64_t ld_kv, uint32_t n_rows, uint32_t n_blocks,
                                                       uint32_t n_items, PageGeom geom, PoolView kpool,
                                                       PoolView vpool, const float* __restrict__ cos,
-                                                      const float* __restrict__ sin) {
+                                                      const float* __restrict__ sin, FastDiv rope_rows) {
   uint32_t blk;
   bool is_v;
   if (!block_of(n_blocks, n_items, blk, is_v)) return;
@@ -195,9 +197,11 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ 
     b = ld16<NT_LOAD>(p + 1);
     if constexpr (ROPE) {
       if (!is_v) {
+        uint32_t chunk, tr;
+        rope_rows.divmod(t, chunk, tr);
         // pairs 8 lane8 .. 8 lane8 + 7 of the head
-        const float4* cp = reinterpret_cast<const float4*>(cos + static_cast<int64_t>(t) * (kHeadDim / 2)) + lane8 * 2;
-        const float4* sp = reinterpret_cast<const float4*>(sin + static_cast<int64_t>(t) * (kHeadDim / 2)) + lane8 * 2;
+        const float4* cp = reinterpret_cast<const float4*>(cos + static_cast<int64_t>(tr) * (kHeadDim / 2)) + lane8 * 2;
+        const float4* sp = reinterpret_cast<const float4*>(sin + static_cast<int64_t>(tr) * (kHeadDim / 2)) + lane8 * 2;
         a = rope_chunk(a, cp[0], sp[0]);
         b = rope_chunk(b, cp[1], sp[1]);
       }
@@ -459,14 +463,17 @@ PageGeom make_geom(int32_t n_heads, const int32_t* page_table, int64_t n_table, 
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// wf_fp8_kv_pack and wf_fp8_kv_pack_rope (cos/sin null: no rotation).
+// wf_fp8_kv_pack and wf_fp8_kv_pack_rope[_tiled] (cos/sin null: no rotation;
+// rope_rows: rows of the table, token t uses row t % rope_rows).
 int launch_pack(const char* fn, const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
-                int64_t ld_kv, const float* cos, const float* sin, const int32_t* page_table, int64_t n_table,
-                int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales, float* v_scales,
-                int64_t pool_pages, void* stream) {
+                int64_t ld_kv, const float* cos, const float* sin, int64_t rope_rows, const int32_t* page_table,
+                int64_t n_table, int32_t page_tokens, uint8_t* k_codes, uint8_t* v_codes, float* k_scales,
+                float* v_scales, int64_t pool_pages, void* stream) {
   if (int st = check_pool_args(fn, n_tokens, n_heads, head_dim, page_table, n_table, page_tokens, pool_pages))
     return st;
   if (n_tokens == 0) return WF_OK;
+  WF_REQUIRE(!cos || (rope_rows > 0 && rope_rows <= n_tokens), WF_E_INVALID,
+             "%s: rope_rows=%lld must be in [1, n_tokens=%lld]", fn, (long long)rope_rows, (long long)n_tokens);
   WF_REQUIRE(k && k_codes && k_scales, WF_E_INVALID, "%s: null K pointer", fn);
   WF_REQUIRE(ld_kv >= static_cast<int64_t>(n_heads) * head_dim && ld_kv % 8 == 0, WF_E_INVALID,
              "%s: ld_kv=%lld must be >= n_heads*head_dim and a multiple of 8", fn, (long long)ld_kv);
@@ -484,11 +491,11 @@ int launch_pack(const char* fn, const void* k, const void* v, int64_t n_tokens, 
   if (cos) {
     hipLaunchKernelGGL((kv_pack_kernel<kPackNtLoad, kPackNtStore, true>), grid, dim3(256), 0, as_stream(stream), k4,
                        v4, ld_kv, n_rows, n_blocks, items, geom, PoolView{k_codes, k_scales},
-                       PoolView{v_codes, v_scales}, cos, sin);
+                       PoolView{v_codes, v_scales}, cos, sin, FastDiv(static_cast<uint32_t>(rope_rows)));
   } else {
     hipLaunchKernelGGL((kv_pack_kernel<kPackNtLoad, kPackNtStore, false>), grid, dim3(256), 0, as_stream(stream), k4,
                        v4, ld_kv, n_rows, n_blocks, items, geom, PoolView{k_codes, k_scales},
-                       PoolView{v_codes, v_scales}, nullptr, nullptr);
+                       PoolView{v_codes, v_scales}, nullptr, nullptr, FastDiv(1));
   }
   return check_launch(fn);
 }
@@ -584,7 +591,7 @@ extern "C" {
 int wf_fp8_kv_pack(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
                    int64_t ld_kv, const int32_t* page_table, int64_t n_table, int32_t page_tokens, uint8_t* k_codes,
                    uint8_t* v_codes, float* k_scales, float* v_scales, int64_t pool_pages, void* stream) {
-  return wf::launch_pack("wf_fp8_kv_pack", k, v, n_tokens, n_heads, head_dim, ld_kv, nullptr, nullptr, page_table,
+  return wf::launch_pack("wf_fp8_kv_pack", k, v, n_tokens, n_heads, head_dim, ld_kv, nullptr, nullptr, 0, page_table,
                          n_table, page_tokens, k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
 }
 
@@ -595,8 +602,19 @@ int wf_fp8_kv_pack_rope(const void* k, const void* v, int64_t n_tokens, int32_t 
   static const char* fn = "wf_fp8_kv_pack_rope";
   WF_REQUIRE(n_tokens == 0 || (cos && sin), WF_E_INVALID, "%s: null RoPE table", fn);
   WF_REQUIRE(wf::aligned16(cos) && wf::aligned16(sin), WF_E_ALIGN, "%s: RoPE tables must be 16-byte aligned", fn);
-  return wf::launch_pack(fn, k, v, n_tokens, n_heads, head_dim, ld_kv, cos, sin, page_table, n_table, page_tokens,
-                         k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
+  return wf::launch_pack(fn, k, v, n_tokens, n_heads, head_dim, ld_kv, cos, sin, n_tokens, page_table, n_table,
+                         page_tokens, k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
+}
+
+int wf_fp8_kv_pack_rope_tiled(const void* k, const void* v, int64_t n_tokens, int32_t n_heads, int32_t head_dim,
+                              int64_t ld_kv, const float* cos, const float* sin, int64_t rope_rows,
+                              const int32_t* page_table, int64_t n_table, int32_t page_tokens, uint8_t* k_codes,
+                              uint8_t* v_codes, float* k_scales, float* v_scales, int64_t pool_pages, void* stream) {
+  static const char* fn = "wf_fp8_kv_pack_rope_tiled";
+  WF_REQUIRE(n_tokens == 0 || (cos && sin), WF_E_INVALID, "%s: null RoPE table", fn);
+  WF_REQUIRE(wf::aligned16(cos) && wf::aligned16(sin), WF_E_ALIGN, "%s: RoPE tables must be 16-byte aligned", fn);
+  return wf::launch_pack(fn, k, v, n_tokens, n_heads, head_dim, ld_kv, cos, sin, rope_rows, page_table, n_table,
+                         page_tokens, k_codes, v_codes, k_scales, v_scales, pool_pages, stream);
 }
 
 

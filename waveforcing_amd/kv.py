@@ -66,12 +66,16 @@ def _as_thd(x: torch.Tensor, name: str) -> torch.Tensor:
     return x
 
 
-def _rope_tables(rope, T: int, D: int, device):
+def _rope_tables(rope, T: int, D: int, device, tiled: bool = False):
+    """Validated (cos, sin) fp32 [R, D/2]: R = T, or with ``tiled`` any R dividing T (token t uses row t % R)."""
     cos, sin = rope
+    R = cos.shape[0] if tiled and cos.dim() == 2 else T
+    if tiled and (R < 1 or T % R):
+        raise ValueError(f"a tiled rope table of {R} rows must divide the {T} tokens")
     for name, t in (("cos", cos), ("sin", sin)):
         on_device = t.device.type == device.type and (device.index is None or t.device.index == device.index)
-        if t.dtype != torch.float32 or tuple(t.shape) != (T, D // 2) or not t.is_contiguous() or not on_device:
-            raise ValueError(f"rope {name} must be contiguous fp32 [{T}, {D // 2}] on {device}")
+        if t.dtype != torch.float32 or tuple(t.shape) != (R, D // 2) or not t.is_contiguous() or not on_device:
+            raise ValueError(f"rope {name} must be contiguous fp32 [{R}, {D // 2}] on {device}")
     return cos, sin
 
 
@@ -100,6 +104,28 @@ class Fp8PagePool:
         self.k_scales = torch.zeros(shape_s, dtype=torch.float32, device=self.device)
         self.v_scales = torch.zeros(shape_s, dtype=torch.float32, device=self.device)
 
+    @classmethod
+    def view_of(cls, base: "Fp8PagePool", first_page: int, n_pages: int) -> "Fp8PagePool":
+        """Pages [first_page, first_page + n_pages) of ``base`` as a pool of their own (shared storage,
+        page ids relative to first_page)."""
+        if first_page < 0 or n_pages < 1 or first_page + n_pages > base.pool_pages:
+            raise ValueError(f"pages [{first_page}, {first_page + n_pages}) outside a pool of {base.pool_pages}")
+        self = cls.__new__(cls)
+        self.pool_pages = n_pages
+        self.n_heads = base.n_heads
+        self.head_dim = base.head_dim
+        self.page_tokens = base.page_tokens
+        self.device = base.device
+        sl = slice(first_page, first_page + n_pages)
+        self.k_codes, self.v_codes = base.k_codes[sl], base.v_codes[sl]
+        self.k_scales, self.v_scales = base.k_scales[sl], base.v_scales[sl]
+        return self
+
+    @staticmethod
+    def bytes_for(pool_pages: int, n_heads: int, head_dim: int, page_tokens: int) -> int:
+        """Device bytes of a pool (K and V codes + scales)."""
+        return 2 * pool_pages * page_tokens * n_heads * (head_dim + 4)
+
     @property
     def nbytes(self) -> int:
         return sum(t.numel() * t.element_size() for t in (self.k_codes, self.v_codes, self.k_scales, self.v_scales))
@@ -111,13 +137,15 @@ class Fp8PagePool:
         return -(-n_tokens // self.page_tokens)
 
     def pack(self, k: torch.Tensor, v: torch.Tensor | None, table: PageTable,
-             rope: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
+             rope: tuple[torch.Tensor, torch.Tensor] | None = None, tiled: bool = False) -> None:
         """Quantize K (and V) [T, H, D] bf16 into the pages listed by ``table``.
 
         With ``rope = (cos, sin)`` (fp32 [T, D/2]), K is rotated first and the
         rotated bf16 values are quantized: the anchor re-RoPE plus slot copy of
         _anchor_working (wave_rt/denoiser/exchange/common.py:70-91,
-        paged.py:222-227) in one kernel.
+        paged.py:222-227) in one kernel.  With ``tiled``, the tables may have
+        R rows for any R dividing T and token t uses row t % R (a batch of equal
+        chunks, e.g. every layer's anchor, in one launch).
         """
         k = _as_thd(k, "k")
         if v is not None:
@@ -135,10 +163,10 @@ class Fp8PagePool:
             k, v = k.contiguous(), v.contiguous()
             ld = H * D
         if rope is not None:
-            cos, sin = _rope_tables(rope, T, D, self.device)
+            cos, sin = _rope_tables(rope, T, D, self.device, tiled)
             _lib.call(
-                "wf_fp8_kv_pack_rope",
-                _lib.ptr(k), _lib.ptr(v), T, H, D, ld, cos.data_ptr(), sin.data_ptr(),
+                "wf_fp8_kv_pack_rope_tiled",
+                _lib.ptr(k), _lib.ptr(v), T, H, D, ld, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                 table.dev.data_ptr(), len(table), self.page_tokens,
                 self.k_codes.data_ptr(), self.v_codes.data_ptr() if v is not None else None,
                 self.k_scales.data_ptr(), self.v_scales.data_ptr() if v is not None else None,
