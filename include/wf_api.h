@@ -197,6 +197,26 @@ int wf_w8a8_linear(const void* x, int64_t m, int64_t k, int64_t ldx,
                    int64_t n, void* y, int64_t ldy, int32_t flags,
                    int8_t* ws_q, float* ws_sx, void* stream);
 
+/* Maximum sizes of wf_w8a8_linear_static's per-GPU workspace. */
+#define WF_W8A8_STATIC_MAX_CODES (64ll << 20)  /* m * k int8 activation codes */
+#define WF_W8A8_STATIC_MAX_ROWS 65536ll        /* m fp32 row scales */
+
+/* wf_w8a8_linear without the workspace arguments, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  The activation codes and row scales go to a workspace held by
+ * the library in a static device array of WF_W8A8_STATIC_MAX_CODES +
+ * 4 * WF_W8A8_STATIC_MAX_ROWS bytes per GPU, kept until the process ends;
+ * the call allocates and frees nothing.  m * k > WF_W8A8_STATIC_MAX_CODES or
+ * m > WF_W8A8_STATIC_MAX_ROWS returns WF_E_SHAPE.  Every call on one GPU
+ * shares that GPU's workspace: calls that overlap on one GPU (on different
+ * streams, or from several threads) race and must be serialized by the
+ * caller.  Results equal wf_w8a8_linear's bit for bit. */
+int wf_w8a8_linear_static(const void* x, int64_t m, int64_t k, int64_t ldx,
+                          const int8_t* qw, const float* sw, const void* bias,
+                          int64_t n, void* y, int64_t ldy, int32_t flags,
+                          void* stream);
+
 /* ------------------------------------------------- W8A8 e4m3, per tensor
  *
  * The reference's WaveFp8Linear arithmetic (wave_rt/runtime/fp8.py:21-61):

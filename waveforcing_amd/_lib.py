@@ -78,6 +78,10 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
         _i64, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
     ],
+    "wf_w8a8_linear_static": [
+        _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+        _i64, _c_void_p, _i64, _i32, _c_void_p,
+    ],
     "wf_fp8_quant_pertensor": [_c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "wf_gemm_fp8_pertensor": [
         _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
@@ -111,6 +115,8 @@ GEMM_GELU_TANH = 1
 FP8_TENSOR_WEIGHT = 0
 FP8_TENSOR_ACT = 1
 FP8_AMAX_PARTIALS = 1024
+W8A8_STATIC_MAX_CODES = 64 << 20
+W8A8_STATIC_MAX_ROWS = 65536
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
