@@ -41,7 +41,7 @@ WINDOW, RF, N_CHUNKS, LAYERS = 21, 4, 11, 2
 
 def _kv(t, rank, layer):
     g = torch.Generator().manual_seed(100000 + 1000 * t + 10 * rank + layer)
-    mk = lambda: (torch.randn((1, T, H, 128), generator=g) * 2).to(torch.bfloat16)
+    mk = lambda: torch.randn((1, T, H, 128), generator=g).to(torch.bfloat16)   # the workload's N(0, 1)
     return mk(), mk(), mk(), mk()          # q, roped K, un-rotated K, V
 
 
