@@ -188,10 +188,17 @@ int wf_gemm_i8(const int8_t* a, const int8_t* w, int64_t m, int64_t n,
                void* y, int64_t ldy, int32_t* acc_out, int32_t flags,
                void* stream);
 
+#define WF_LINEAR_GELU_INPUT 2
+
 /* Fused W8A8 linear: wf_act_quant_i8 of x into the caller's workspace
  * (ws_q int8 [m][k], ws_sx fp32 [m]) followed by wf_gemm_i8 against the
  * pre-quantized weight (qw int8 [n][k], sw fp32 [n]).  The call contract of
- * WaveFp8Linear.forward (wave_rt/runtime/fp8.py:58-61) on 2-D input. */
+ * WaveFp8Linear.forward (wave_rt/runtime/fp8.py:58-61) on 2-D input.
+ * flags: WF_GEMM_GELU_TANH applies GELU(tanh) to the output (as wf_gemm_i8);
+ * WF_LINEAR_GELU_INPUT quantizes bf16(GELU(tanh)(x)) in place of x -- the FFN
+ * activation between fc_in and fc_out (causal_model.py:342-344) applied by
+ * fc_out's input quantizer, with the values fc_in's GELU epilogue would have
+ * produced. */
 int wf_w8a8_linear(const void* x, int64_t m, int64_t k, int64_t ldx,
                    const int8_t* qw, const float* sw, const void* bias,
                    int64_t n, void* y, int64_t ldy, int32_t flags,

@@ -65,6 +65,8 @@ def _gemm_case(M, N, K, seed, bias=True, gelu=False):
     (4680, 4608, 1536),   # fused QKV
     (4680, 1536, 8960),   # fc_out
     (1, 4, 16), (17, 132, 48), (300, 256, 1552), (513, 1540, 272),
+    (3000, 3204, 272),    # more tiles than CUs (persistent kernel), partial tiles, N % 8 == 4: 8-byte stores
+    (2050, 8196, 160),    # persistent, 561 tiles, K tail of 32 bytes
 ])
 def test_gemm_exact(M, N, K):
     y, acc, oy, oacc = _gemm_case(M, N, K, seed=M + N + K)
@@ -113,6 +115,42 @@ def test_gemm_gelu_within_tolerance():
     rel = (y.float() - oy.float()).norm() / oy.float().norm()
     assert rel < 1e-2, float(rel)
     assert float((y.float() - oy.float()).abs().max()) <= 2 ** -6 * float(oy.float().abs().max())
+
+
+def _linear(x, qw, sw, b, flags):
+    from waveforcing_amd import _lib
+    M, K = x.shape
+    N = qw.shape[0]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    ws_q = torch.empty((M, K), dtype=torch.int8, device=DEV)
+    ws_s = torch.empty((M,), dtype=torch.float32, device=DEV)
+    _lib.call("wf_w8a8_linear", x.data_ptr(), M, K, x.stride(0), qw.data_ptr(), sw.data_ptr(), b.data_ptr(), N,
+              y.data_ptr(), y.stride(0), flags, ws_q.data_ptr(), ws_s.data_ptr(), _lib.stream_handle(DEV))
+    return y
+
+
+def test_linear_gelu_input_equals_gelu_epilogue_and_oracle():
+    """fc_in -> GELU -> fc_out at the 1.3B shapes: GELU applied by fc_out's input quantizer
+    (WF_LINEAR_GELU_INPUT) equals, bit for bit, GELU applied in fc_in's GEMM epilogue, and the oracle's
+    F.gelu(tanh) on the bf16 fc_in output within the GELU tolerance."""
+    import torch.nn.functional as F
+
+    from waveforcing_amd import _lib
+    M, D, FF = 4680, 1536, 8960
+    x = inputs.outlier_activations(M, D, seed=31, chan_seed=32)
+    w1, b1 = inputs.linear_weights(FF, D, w_seed=33, b_seed=34)
+    w2, b2 = inputs.linear_weights(D, FF, w_seed=35, b_seed=36)
+    qx, sx = _quant_rows_i8(x.to(DEV))
+    q1, s1 = _quant_rows_i8(w1.to(DEV))
+    q2, s2 = _quant_rows_i8(w2.to(DEV))
+    pre = gemm_i8(qx, q1, sx, s1, b1.to(DEV))
+    post = gemm_i8(qx, q1, sx, s1, b1.to(DEV), gelu=True)
+    got = _linear(pre, q2, s2, b2.to(DEV), _lib.LINEAR_GELU_INPUT)
+    want = _linear(post, q2, s2, b2.to(DEV), 0)
+    assert torch.equal(got, want)
+    ref = olin.i8_linear(F.gelu(pre.cpu().float(), approximate="tanh").to(torch.bfloat16), w2, b2)
+    rel = (got.cpu().float() - ref.float()).norm() / ref.float().norm()
+    assert rel < 1e-2, float(rel)
 
 
 def test_linear_module_matches_oracle():

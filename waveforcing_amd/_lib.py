@@ -112,6 +112,7 @@ SIGNATURES: dict[str, list] = {
 }
 
 GEMM_GELU_TANH = 1
+LINEAR_GELU_INPUT = 2
 FP8_TENSOR_WEIGHT = 0
 FP8_TENSOR_ACT = 1
 FP8_AMAX_PARTIALS = 1024

@@ -14,7 +14,8 @@ counterpart of the block WaveRT's SGLang model runs (SGLang is not vendored), wi
   (the single-GPU form of the paged exchange, paged.py:206-247);
 * text cross-attention over the cached 512-token K/V (crossattn_cache,
   model.py:174-183) in the dense-bf16 variant of the attention kernel;
-* GELU(tanh) fused into the fc_in epilogue; gated residuals in bf16.
+* GELU(tanh) of fc_in's output fused into fc_out's input quantization; gated
+  residuals in bf16.
 
 Every step is a HIP kernel from libwf_mi355x.so; torch only allocates and
 slices tensors.
@@ -152,12 +153,14 @@ def apply_pending_residual(x: torch.Tensor, pending, frame_tokens: int) -> torch
     return x
 
 
-def _linear_i8(x, lin: QLinear, ws_q, ws_s, out, gelu=False):
-    """W8A8 linear of bf16 x [M, K] into out [M, N] via the fused C entry point."""
+def _linear_i8(x, lin: QLinear, ws_q, ws_s, out, gelu=False, gelu_input=False):
+    """W8A8 linear of bf16 x [M, K] into out [M, N] via the fused C entry point; ``gelu`` applies GELU(tanh) to
+    the output, ``gelu_input`` to x before its quantization."""
     M, K = x.shape
     N = lin.w.shape[0]
+    flags = (_lib.GEMM_GELU_TANH if gelu else 0) | (_lib.LINEAR_GELU_INPUT if gelu_input else 0)
     _lib.call("wf_w8a8_linear", x.data_ptr(), M, K, x.stride(0), lin.w.data_ptr(), lin.s.data_ptr(),
-              _lib.ptr(lin.b), N, out.data_ptr(), out.stride(0), _lib.GEMM_GELU_TANH if gelu else 0,
+              _lib.ptr(lin.b), N, out.data_ptr(), out.stride(0), flags,
               ws_q.data_ptr(), ws_s.data_ptr(), _lib.stream_handle(x.device))
     return out
 
@@ -316,10 +319,11 @@ class QuantizedWanBlock:
         attn_dense_bf16(ws["cq"].view(T, H, hd), tk, tv, out=ws["attn"].view(T, H, hd))
         _linear_i8(ws["attn"], self.co, aq, as_, ws["y"])
 
-        # residual + LN2 + modulation + quant -> fc_in (+GELU) -> fc_out
+        # residual + LN2 + modulation + quant -> fc_in -> GELU + quant -> fc_out: the GELU(tanh) of fc_in's bf16
+        # output runs in fc_out's input quantizer (the same values the GEMM epilogue would store)
         _ln_quant(x, dim, ft, aq, as_, shift=e3, scale=e4, res_y=ws["y"])
-        gemm_i8(aq, self.fc_in.w, as_, self.fc_in.s, self.fc_in.b, gelu=True, out=ws["ffn"])
-        _linear_i8(ws["ffn"], self.fc_out, ws["fq"], as_, ws["y"])
+        gemm_i8(aq, self.fc_in.w, as_, self.fc_in.s, self.fc_in.b, out=ws["ffn"])
+        _linear_i8(ws["ffn"], self.fc_out, ws["fq"], as_, ws["y"], gelu_input=True)
         if defer_residual:
             return x, (ws["y"], e5)
         _gate_residual(x, ws["y"], e5, ft)

@@ -1,4 +1,5 @@
 // Status reporting of the C ABI and the elementwise FP8 cast entry points.
+#include <atomic>
 #include <cstring>
 
 #include "fp8_codec.hpp"
@@ -17,6 +18,18 @@ int set_error(int status, const char* fmt, ...) {
   vsnprintf(error_buffer(), 512, fmt, ap);
   va_end(ap);
   return status;
+}
+
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 int check_launch(const char* what) {

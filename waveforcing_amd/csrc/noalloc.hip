@@ -80,12 +80,13 @@ extern "C" int wf_w8a8_linear_static(const void* x, int64_t m, int64_t k, int64_
                  (reinterpret_cast<uintptr_t>(sw) & 15u) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0 &&
                  (reinterpret_cast<uintptr_t>(bias) & 7u) == 0,
              WF_E_ALIGN, "%s: x, qw, sw must be 16-byte and y, bias 8-byte aligned", fn);
-  WF_REQUIRE((flags & ~1) == 0, WF_E_INVALID, "%s: unknown flags 0x%x", fn, flags);
+  WF_REQUIRE((flags & ~(WF_GEMM_GELU_TANH | WF_LINEAR_GELU_INPUT)) == 0, WF_E_INVALID, "%s: unknown flags 0x%x", fn,
+             flags);
   uint8_t* base = nullptr;
   if (int rc = wf::scratch_of_current_device(&base, fn)) return rc;
   int8_t* q = reinterpret_cast<int8_t*>(base);
   float* sx = reinterpret_cast<float*>(base + kScratchCodeBytes);   // 256-byte aligned (the code region is)
   hipStream_t st = wf::as_stream(stream);
-  if (int rc = wf::launch_quant_rows_i8(x, m, k, ldx, q, k, sx, st)) return rc;
-  return wf::launch_gemm_i8(q, qw, m, n, k, sx, sw, bias, y, ldy, nullptr, flags & 1, st);
+  if (int rc = wf::launch_quant_rows_i8(x, m, k, ldx, q, k, sx, st, (flags & WF_LINEAR_GELU_INPUT) != 0)) return rc;
+  return wf::launch_gemm_i8(q, qw, m, n, k, sx, sw, bias, y, ldy, nullptr, flags & WF_GEMM_GELU_TANH, st);
 }

@@ -12,6 +12,12 @@
 // quotient for every fp32 x and s (rows::quant_i8 gives the argument), then
 // rounded half to even, so the result is round_half_even(RN(x / s)) exactly.
 //
+// With GELU, every element is first replaced by bf16(gelu_tanh(x)) (the
+// FFN activation applied to fc_in's bf16 output, causal_model.py:342-344)
+// and those values are quantized: the same values the fc_in GEMM's GELU
+// epilogue would have stored, so moving the activation here changes no bit
+// and takes its VALU work off the GEMM's critical path.
+//
 // Rows up to 16384 wide run on the row engine of rows.hpp (one wave per row
 // up to 2048, one workgroup per row above; the row stays in registers
 // between the absmax reduction and the quantization pass).  Wider rows use
@@ -40,6 +46,22 @@ __device__ inline float amax8(const uint4& a) {
   return m;
 }
 
+// 8 bf16 values -> bf16(gelu_tanh(x)) of each (the GEMM epilogue's arithmetic).
+__device__ inline uint4 gelu8(const uint4& a) {
+  float v[8];
+  rows::unpack8(a, v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = gelu_tanh(v[i]);
+  return rows::pack8(v);
+}
+
+template <bool GELU>
+__device__ inline uint4 load_chunk(const uint16_t* p) {
+  const uint4 a = *reinterpret_cast<const uint4*>(p);
+  if constexpr (GELU) return gelu8(a);
+  return a;
+}
+
 // 8 bf16 values -> 8 int8 codes (rows::quant8_i8 with rd = RN64(1/s)).
 __device__ inline uint2 quant8(const uint4& a, double rd) {
   float v[8];
@@ -48,6 +70,7 @@ __device__ inline uint2 quant8(const uint4& a, double rd) {
 }
 
 // K % 8 == 0 (checked at the entry point): every 8-element chunk is whole.
+template <bool GELU>
 __global__ __launch_bounds__(kThreads) void quant_rows_i8_kernel(const uint16_t* __restrict__ x, int64_t M,
                                                                  int64_t K, int64_t ldx, int8_t* __restrict__ q,
                                                                  int64_t ldq, float* __restrict__ scales) {
@@ -63,11 +86,11 @@ __global__ __launch_bounds__(kThreads) void quant_rows_i8_kernel(const uint16_t*
 #pragma unroll
   for (int c = 0; c < kRegChunks; ++c) {
     const int64_t ch = lane + 64 * c;
-    reg[c] = ch < n_chunks ? *reinterpret_cast<const uint4*>(row + ch * 8) : make_uint4(0, 0, 0, 0);
+    reg[c] = ch < n_chunks ? load_chunk<GELU>(row + ch * 8) : make_uint4(0, 0, 0, 0);
     amax = fmaxf(amax, amax8(reg[c]));
   }
   for (int64_t ch = lane + 64 * kRegChunks; ch < n_chunks; ch += 64)
-    amax = fmaxf(amax, amax8(*reinterpret_cast<const uint4*>(row + ch * 8)));
+    amax = fmaxf(amax, amax8(load_chunk<GELU>(row + ch * 8)));
   amax = wave_max(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-8f);
   const double rd = rows::i8_recip(s);
@@ -78,11 +101,11 @@ __global__ __launch_bounds__(kThreads) void quant_rows_i8_kernel(const uint16_t*
     if (ch < n_chunks) *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(reg[c], rd);
   }
   for (int64_t ch = lane + 64 * kRegChunks; ch < n_chunks; ch += 64)
-    *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(*reinterpret_cast<const uint4*>(row + ch * 8), rd);
+    *reinterpret_cast<uint2*>(qrow + ch * 8) = quant8(load_chunk<GELU>(row + ch * 8), rd);
 }
 
 // Row-engine variant: LPR lanes per row, NC chunks of 8 per lane.
-template <int LPR, int NC>
+template <int LPR, int NC, bool GELU>
 __global__ __launch_bounds__(256) void quant_rows_i8_row_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                                 int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
                                                                 float* __restrict__ scales) {
@@ -100,6 +123,10 @@ __global__ __launch_bounds__(256) void quant_rows_i8_row_kernel(const uint16_t* 
     const int ch = lane + LPR * c;
     reg[c] = ch < n_chunks ? rows::ld16(row + ch * 8) : make_uint4(0, 0, 0, 0);
   }
+  if constexpr (GELU) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) reg[c] = gelu8(reg[c]);
+  }
 #pragma unroll
   for (int c = 0; c < NC; ++c) amax = fmaxf(amax, amax8(reg[c]));
   amax = rows::row_max_nonneg<LPR>(amax, red);
@@ -114,22 +141,31 @@ __global__ __launch_bounds__(256) void quant_rows_i8_row_kernel(const uint16_t* 
   }
 }
 
-}  // namespace
-
-int launch_quant_rows_i8(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* scales,
-                         hipStream_t stream) {
+template <bool GELU>
+void launch_rows(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* scales,
+                 hipStream_t stream) {
   int lpr = 0, nc = 0;
   if (rows::pick_shape(K / 8, lpr, nc)) {
     const uint32_t grid = static_cast<uint32_t>((M + 256 / lpr - 1) / (256 / lpr));
     rows::dispatch_shape(lpr, nc, [&](auto L, auto C) {
-      hipLaunchKernelGGL((quant_rows_i8_row_kernel<decltype(L)::value, decltype(C)::value>), dim3(grid), dim3(256),
-                         0, stream, static_cast<const uint16_t*>(x), static_cast<int>(M), static_cast<int>(K), ldx, q,
-                         ldq, scales);
+      hipLaunchKernelGGL((quant_rows_i8_row_kernel<decltype(L)::value, decltype(C)::value, GELU>), dim3(grid),
+                         dim3(256), 0, stream, static_cast<const uint16_t*>(x), static_cast<int>(M),
+                         static_cast<int>(K), ldx, q, ldq, scales);
     });
   } else {
-    hipLaunchKernelGGL(quant_rows_i8_kernel, dim3(static_cast<uint32_t>((M + kRowsPerBlock - 1) / kRowsPerBlock)),
+    hipLaunchKernelGGL(quant_rows_i8_kernel<GELU>, dim3(static_cast<uint32_t>((M + kRowsPerBlock - 1) / kRowsPerBlock)),
                        dim3(kThreads), 0, stream, static_cast<const uint16_t*>(x), M, K, ldx, q, ldq, scales);
   }
+}
+
+}  // namespace
+
+int launch_quant_rows_i8(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* scales,
+                         hipStream_t stream, bool gelu) {
+  if (gelu)
+    launch_rows<true>(x, M, K, ldx, q, ldq, scales, stream);
+  else
+    launch_rows<false>(x, M, K, ldx, q, ldq, scales, stream);
   return check_launch("wf_act_quant_i8");
 }
 

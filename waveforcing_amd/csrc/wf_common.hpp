@@ -28,6 +28,10 @@ int check_launch(const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Compute units of the current device (looked up once per device; 0 if the
+// query fails, which sends callers to their non-persistent launch).
+int device_cus();
+
 // ------------------------------------------------------------------- bf16
 // bf16 -> fp32 is exact: the bf16 bits are the high half of the fp32 bits.
 __device__ __host__ inline float bf16_lo_to_f32(uint32_t packed) {
@@ -82,6 +86,17 @@ __device__ inline uint32_t pack_bf16x2_hw(float a, float b) {
   typedef __bf16 b2 __attribute__((ext_vector_type(2)));
   const f2 v = {a, b};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
+}
+
+// GELU(approximate='tanh'): 0.5 x (1 + tanh(u)) = x / (1 + e^{-2u}) with
+// u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as x * rcp(1 + 2^{-2u log2 e})
+// on the hardware exponential and reciprocal (relative error ~3e-7 against
+// the tanh form; x -> -inf gives -0, x -> +inf gives x).  The FFN activation
+// of the Wan block (naive_rt/rolling_forcing/wan/modules/causal_model.py:342-344).
+__device__ inline float gelu_tanh(float x) {
+  const float inner = x * fmaf(0.044715f, x * x, 1.0f);     // x + 0.044715 x^3
+  const float e = __builtin_amdgcn_exp2f(-2.3022082f * inner);  // 2 sqrt(2/pi) log2(e) = 2.3022082
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // ------------------------------------------------------- wave64 reductions
