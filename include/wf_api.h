@@ -369,6 +369,48 @@ int wf_qk_norm_rope_kv_pack(void* q, int64_t ld_q, const void* norm_q,
                             float* v_scales, int64_t pool_pages, void* stream);
 
 /* ---------------------------------------------------------------------
+ * The DiT around the blocks (bf16, as the reference runs it)
+ * ------------------------------------------------------------------- */
+
+#define WF_BF16_SILU_IN 1    /* SiLU on a's elements (rounded to bf16) first */
+#define WF_BF16_SILU_OUT 2   /* SiLU on the bf16 output, rounded to bf16 */
+#define WF_BF16_GELU_OUT 4   /* GELU(tanh) on the bf16 output, rounded to bf16 */
+
+/* bf16 GEMM y[m][n] = act_out(bf16(sum_k act_in(a[m,k]) * w[n,k] + bias[n]))
+ * with fp32 accumulation: a [m][k] (row stride lda), w [n][k] dense (nn.Linear
+ * layout), bias bf16 [n] or NULL, y bf16 (row stride ldy).  k, lda % 8 == 0;
+ * n, ldy % 4 == 0; a, w 16-byte and y 8-byte aligned.  The bf16 linears of
+ * the Wan DiT outside its blocks: the text embedding (Linear, GELU(tanh),
+ * Linear), the time embedding (Linear, SiLU, Linear), the time projection
+ * (SiLU, Linear), the head's Linear, and the patch embedding over
+ * wf_patchify_bf16's patches (naive_rt/rolling_forcing/wan/modules/
+ * causal_model.py:406-433,517-528). */
+int wf_gemm_bf16(const void* a, int64_t m, int64_t k, int64_t lda,
+                 const void* w, int64_t n, const void* bias, void* y,
+                 int64_t ldy, int32_t flags, void* stream);
+
+/* Patches of the Conv3d patch embedding (kernel = stride = (1, 2, 2)):
+ * x bf16 [b][c][f][h][w] -> out bf16 [b][f * (h/2) * (w/2)][c * 4] with
+ * out[b][t][4 ci + 2 kh + kw] = x[b][ci][fi][2 yi + kh][2 xi + kw] for token
+ * t = (fi, yi, xi) -- the (c, kt, kh, kw) order of the Conv3d weight, so the
+ * embedding is wf_gemm_bf16 against the weight viewed as [dim][4 c]
+ * (causal_model.py:517-518, the flatten(2).transpose(1, 2) of :826-830).
+ * h and w even. */
+int wf_patchify_bf16(const void* x, int64_t b, int32_t c, int32_t f,
+                     int32_t h, int32_t w, void* out, void* stream);
+
+/* Unpatchify the head output and convert the flow prediction to x0:
+ * flow[b][ci][fi][2 yi + q][2 xi + r] = head[b][t(fi, yi, xi)][(2 q + r) c + ci]
+ * ('fhwpqrc->cfphqwr', causal_model.py:1080-1103, patch (1, 2, 2)), then
+ * x0 = xt - sigma * flow in float64 (wan_wrapper.py:169-193), converted to
+ * bf16 through float32 as torch converts float64, and written as
+ * x0 [b][f][c][h][w] (the (B, T, C, H, W) x0 of forward_chunk,
+ * wave_rt/runtime/backend.py:456-490).  xt bf16 [b][c][f][h][w]; h, w even. */
+int wf_unpatchify_flow_x0_bf16(const void* head, const void* xt, int64_t b,
+                               int32_t c, int32_t f, int32_t h, int32_t w,
+                               double sigma, void* x0, void* stream);
+
+/* ---------------------------------------------------------------------
  * Re-noising for the next DMD step
  * ------------------------------------------------------------------- */
 

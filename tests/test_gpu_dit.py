@@ -1,0 +1,126 @@
+"""GPU parity of the DiT layers around the blocks against the CPU oracle (oracle/dit.py).
+
+* wf_gemm_bf16 at the shapes of the patch embedding, text and time
+  embeddings, time projection and head: within one bf16 ulp of the oracle's
+  fp32-accumulated linear (a different summation order may move the single
+  rounding by one ulp) in all but a few elements; with SiLU / GELU(tanh), whose
+  exponential differs from the CPU's, relative L2 <= 1e-3;
+* patch gather: bit-exact;
+* unpatchify + flow -> x0: bit-exact (float64 arithmetic, float32 route to bf16);
+* one chunk's whole forward (QuantizedWanDiT.forward_chunk: patch embedding,
+  time embedding, 2 blocks over the paged exchange, head, x0) against the
+  oracle chained over the same parameters, at a small width and at the 1.3B
+  width on a 4680-token chunk: relative L2 <= 1e-2 (the block bar).
+"""
+
+import pytest
+import torch
+
+from oracle import block as ob
+from oracle import dit as od
+from oracle import kv as okv
+from waveforcing_amd import _lib
+from waveforcing_amd.block import QuantizedWanBlock, random_block_params
+from waveforcing_amd.dit import QuantizedWanDiT, gemm_bf16, random_dit_params
+from waveforcing_amd.exchange import PagedExchange
+from waveforcing_amd.schedule import FlowMatchSchedule
+from waveforcing_amd.stack import QuantizedWanStack
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+BF16 = torch.bfloat16
+
+
+def _ulp(x):
+    return torch.pow(2.0, torch.floor(torch.log2(x.abs().clamp(min=2.0 ** -100))) - 7)
+
+
+@pytest.mark.parametrize("M,K,N,silu_in,act", [
+    (4680, 64, 1536, False, None),      # patch embedding
+    (512, 4096, 1536, False, "gelu"),   # text embedding, first linear
+    (512, 1536, 1536, False, None),     # text embedding, second linear
+    (3, 256, 1536, False, "silu"),      # time embedding, first linear
+    (3, 1536, 9216, True, None),        # time projection (SiLU first)
+    (4680, 1536, 64, False, None),      # head
+    (4680, 5120, 64, False, None),      # 14B head
+    (37, 40, 12, False, None), (1, 8, 4, True, "silu"),
+])
+def test_gemm_bf16_matches_oracle_linear(M, K, N, silu_in, act):
+    g = torch.Generator().manual_seed(M + K + N)
+    a = torch.randn((M, K), generator=g).to(BF16)
+    w = (torch.randn((N, K), generator=g) * K ** -0.5).to(BF16)
+    b = (torch.randn((N,), generator=g) * 0.1).to(BF16)
+    got = gemm_bf16(a.to(DEV), w.to(DEV), b.to(DEV), silu_in=silu_in, act_out=act).cpu().float()
+    want = od.linear(a, w, b, act_out=act, silu_in=silu_in).float()
+    rel = ((got - want).norm() / want.norm()).item()
+    print(f"rel L2 {rel:.2e}")
+    if act is None and not silu_in:
+        assert ((got - want).abs() <= _ulp(want) + 1e-6).all()
+        assert (got == want).double().mean() > 0.98
+    assert rel <= 1e-3
+
+
+def test_patchify_exact():
+    lat = torch.randn((1, 16, 3, 60, 104), generator=torch.Generator().manual_seed(1)).to(BF16)
+    out = torch.empty((3 * 30 * 52, 64), dtype=BF16, device=DEV)
+    lat_d = lat.to(DEV)   # held: a temporary's memory could be handed to the next allocation before the launch
+    _lib.call("wf_patchify_bf16", lat_d.data_ptr(), 1, 16, 3, 60, 104, out.data_ptr(), _lib.stream_handle(DEV))
+    assert torch.equal(out.cpu(), od.patchify(lat[0]))
+
+
+@pytest.mark.parametrize("sigma", [0.0, 15 / 16, 0.8333333333333334, 0.625, 1.0])
+def test_unpatchify_flow_x0_exact(sigma):
+    g = torch.Generator().manual_seed(2)
+    head = torch.randn((3 * 30 * 52, 64), generator=g).to(BF16)
+    xt = torch.randn((1, 16, 3, 60, 104), generator=g).to(BF16)
+    x0 = torch.empty((1, 3, 16, 60, 104), dtype=BF16, device=DEV)
+    head_d, xt_d = head.to(DEV), xt.to(DEV)
+    _lib.call("wf_unpatchify_flow_x0_bf16", head_d.data_ptr(), xt_d.data_ptr(), 1, 16, 3, 60, 104,
+              float(sigma), x0.data_ptr(), _lib.stream_handle(DEV))
+    want = od.flow_to_x0(od.unpatchify(head, (3, 30, 52)), xt[0], sigma).permute(1, 0, 2, 3)
+    assert torch.equal(x0.cpu()[0], want)
+
+
+def _dit_case(dim, heads, ffn, layers, H, W, seed):
+    bparams = [random_block_params(dim, ffn, seed=seed + i) for i in range(layers)]
+    dparams = random_dit_params(dim, seed=seed + 100)
+    g = torch.Generator().manual_seed(seed + 200)
+    noisy = torch.randn((1, 16, 3, H, W), generator=g).to(BF16)
+    ctx = (torch.randn((300, 4096), generator=g) * 0.5).to(BF16)
+    return bparams, dparams, noisy, ctx
+
+
+@pytest.mark.parametrize("dim,heads,ffn,H,W", [(256, 2, 512, 16, 16), (1536, 12, 8960, 60, 104)])
+def test_dit_forward_chunk_matches_oracle(dim, heads, ffn, H, W):
+    layers, t = 2, 937.5
+    bparams, dparams, noisy, ctx = _dit_case(dim, heads, ffn, layers, H, W, seed=11)
+    hp, wp = H // 2, W // 2
+    page = hp * wp
+    T = 3 * page
+    # GPU: a fresh exchange (no clean chunks): the first denoise pass of chunk 0 attends to itself
+    blocks = [QuantizedWanBlock(p, heads, DEV) for p in bparams]
+    stack = QuantizedWanStack(blocks, PagedExchange(layers, heads, page, 3, 21, rf_step=4, device=DEV))
+    dit = QuantizedWanDiT(dparams, stack)
+    emb = dit.set_text(ctx.to(DEV))
+    x0 = dit.forward_chunk(noisy.to(DEV), t, chunk=0).cpu()[0]
+    # oracle
+    oemb = od.text_embed(dparams, ctx)
+    emb_rel = ((emb.cpu().float() - oemb.float()).norm() / oemb.float().norm()).item()
+    tkv = [ob.text_kv(p, oemb, heads) for p in bparams]
+
+    def stack_fn(x, e0):
+        for L, p in enumerate(bparams):
+            pk, pv = okv.new_pool(3, page, heads, 128), okv.new_pool(3, page, heads, 128)
+            x = ob.block_forward(p, x, e0, (3, hp, wp), 0, pk, pv, [0, 1, 2], [0, 1, 2], T, page, *tkv[L], heads)
+        return x
+
+    sched = FlowMatchSchedule()
+    sig, ts = sched.sigmas, sched.timesteps
+    want = od.dit_forward(dparams, stack_fn, noisy[0], t, od.sigma_x0(sig, ts, t))
+    rel = ((x0.float() - want.float()).norm() / want.float().norm()).item()
+    # the flow part alone (x0 - xt = -sigma * flow) carries the blocks' differences
+    xt = noisy[0].permute(1, 0, 2, 3).float()
+    frel = (((x0.float() - xt) - (want.float() - xt)).norm() / (want.float() - xt).norm()).item()
+    print(f"text embedding rel L2 {emb_rel:.2e}; x0 rel L2 {rel:.2e}; flow part rel L2 {frel:.2e}")
+    assert emb_rel <= 1e-2
+    assert frel <= 1e-2

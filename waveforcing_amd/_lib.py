@@ -108,6 +108,10 @@ SIGNATURES: dict[str, list] = {
     "wf_rmsnorm_rope": [
         _c_void_p, _i64, _i32, _i64, _i32, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
     ],
+    "wf_gemm_bf16": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p],
+    "wf_patchify_bf16": [_c_void_p, _i64, _i32, _i32, _i32, _i32, _c_void_p, _c_void_p],
+    "wf_unpatchify_flow_x0_bf16": [_c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32, ctypes.c_double, _c_void_p,
+                                   _c_void_p],
     "wf_gate_residual": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i32, _i32, _c_void_p],
 }
 
@@ -116,6 +120,9 @@ LINEAR_GELU_INPUT = 2
 FP8_TENSOR_WEIGHT = 0
 FP8_TENSOR_ACT = 1
 FP8_AMAX_PARTIALS = 1024
+BF16_SILU_IN = 1
+BF16_SILU_OUT = 2
+BF16_GELU_OUT = 4
 W8A8_STATIC_MAX_CODES = 64 << 20
 W8A8_STATIC_MAX_ROWS = 65536
 

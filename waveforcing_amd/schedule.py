@@ -54,6 +54,13 @@ class FlowMatchSchedule:
             raise ValueError(f"denoising steps {list(steps)} fall outside the 1000-step table")
         return [float(x) for x in t[idx]]
 
+    def sigma_x0(self, t: float) -> float:
+        """sigma of the timestep nearest to t as the flow -> x0 conversion picks it: in float64 over the
+        float32 table (wan_wrapper.py:182-190)."""
+        ts = self.timesteps.double()
+        idx = int(torch.argmin((ts - float(t)).abs()))
+        return float(self.sigmas.double()[idx])
+
     def sigma_at(self, t: float) -> float:
         """sigma of the timestep nearest to t (the first on a tie), as add_noise picks it."""
         tt = float(t) * torch.ones([1], dtype=torch.long)
