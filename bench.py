@@ -356,6 +356,46 @@ def bench_stack(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
     return out
 
 
+def bench_dit(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
+    """The whole DiT forward of one chunk from its noisy latent [1, 16, 3, 60, 104] to x0 (patch embedding, time
+    embedding, the 30 blocks over the paged exchange, head, unpatchify and flow -> x0), as rank 0's pass of the
+    same steady-state tick as bench_stack (37440-key context), at the first DMD timestep."""
+    from waveforcing_amd.dit import QuantizedWanDiT, random_dit_params
+    from waveforcing_amd.exchange import TickPlan
+    from waveforcing_amd.stack import QuantizedWanStack
+
+    frames, H, W = 3, 60, 104
+    st = QuantizedWanStack.random(preset, seed=100, device=dev, tokens_per_frame=(H // 2) * (W // 2),
+                                  frames_per_chunk=frames, max_attn_frames=21, rf_step=4)
+    ex = st.exchange
+    dit = QuantizedWanDiT(random_dit_params(st.blocks[0].dim, seed=7, device=dev), st)
+    g = torch.Generator(device=dev).manual_seed(6)
+    dit.set_text(torch.randn((512, 4096), generator=g, device=dev).to(torch.bfloat16))
+    noisy = torch.randn((1, 16, frames, H, W), generator=g, device=dev).to(torch.bfloat16)
+    steps_t = dit.schedule.warp()
+    for c in range(8):
+        dit.forward_chunk(noisy, 0.0, c, store=True)
+    plan = TickPlan(STEADY_TICK, [0, 1, 2, 3], True, (STEADY_TICK - 3) * frames, 4 * frames)
+    ex.begin_tick(plan)
+    dit.run_pass(noisy, 0.0, ex.store_pass(), want_x0=False)
+    for r in (3, 2, 1):
+        dit.run_pass(noisy, steps_t[r], ex.denoise_pass(r))
+    p0 = ex.denoise_pass(0)
+    x0 = torch.empty((1, frames, 16, H, W), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        dit.run_pass(noisy, steps_t[0], p0, x0_out=x0)
+
+    ms = _timed(step, steps, warmup)
+    ex.abort_tick()
+    T = frames * (H // 2) * (W // 2)
+    out = {"ms": ms, "layers": len(st.blocks), "tokens": T, "latent": [1, 16, frames, H, W],
+           "timestep": steps_t[0], "tokens_per_s": T / (ms * 1e-3)}
+    del dit, st
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_copy(steps: int, warmup: int, dev: str):
     """A plain device copy of 1 GiB (read 1 GiB + write 1 GiB): calibrates the HBM byte counters."""
     src = torch.empty((1 << 30,), dtype=torch.uint8, device=dev).fill_(1)
@@ -516,7 +556,8 @@ def main() -> None:
     ap.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
                     help="minimum untimed warm-up of the KV workloads (profiler runs use 0)")
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
-                                       "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "copy"],
+                                       "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
+                                       "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -535,6 +576,7 @@ def main() -> None:
               "block_1p3b": lambda s, w, d: bench_block("1.3b", s, w, d),
               "block_14b": lambda s, w, d: bench_block("14b", s, w, d), "exchange_1p3b": bench_exchange,
               "stack_1p3b": bench_stack, "stack_14b": lambda s, w, d: bench_stack(s, w, d, "14b"),
+              "dit_1p3b": bench_dit,
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
@@ -548,6 +590,7 @@ def main() -> None:
     xch = bench_exchange(max(5, args.steps // 5), 2, dev)
     stk = bench_stack(max(3, args.steps // 10), 1, dev)
     stk14 = bench_stack(3, 1, dev, "14b")
+    dit = bench_dit(max(3, args.steps // 10), 1, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     cpu_extra = None if args.no_cpu_baseline else cpu_baseline_extra()
     # one launch per step: the launch duration is the step time
@@ -633,6 +676,11 @@ def main() -> None:
                               "live + self + 3 in-flight = 37440 keys, fused in-block K/V pack per layer), and the "
                               "whole tick (store pass + 4 denoise passes, 2 anchor re-RoPEs); random init drawn on "
                               "the GPU",
+            "dit_forward_1p3b_ms_per_chunk": round(dit["ms"], 3),
+            "dit_forward_1p3b_tokens_per_s": round(dit["tokens_per_s"], 1),
+            "dit_forward_note": "the whole Wan-1.3B DiT forward of one chunk, noisy latent [1,16,3,60,104] -> x0 "
+                                "(patch embedding, time embedding, 30 blocks, head, unpatchify, flow -> x0) as rank "
+                                "0's pass of the same steady-state tick (37440-key context), timestep 1000",
             "dit_block_1p3b_ms_per_chunk": round(b13["ms"], 4),
             "dit_block_14b_ms_per_chunk": round(b14["ms"], 4),
             "dit_block_note": "one block, 4680-token 3-frame chunk, 37440-key FP8 paged self-attn context, "

@@ -157,10 +157,15 @@ def last_error() -> str:
     return load().wf_last_error().decode(errors="replace")
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Invoke ``name`` and raise ``RuntimeError`` on a non-zero status."""
-    lib = load()
-    status = getattr(lib, name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    status = fn(*args)
     if status != 0:
         raise RuntimeError(f"{name} failed (status {status}): {last_error()}")
 
@@ -171,7 +176,9 @@ def ptr(t) -> int | None:
 
 
 def stream_handle(device=None) -> int:
-    """hipStream_t of torch's current stream on ``device``."""
+    """hipStream_t of torch's current stream on ``device`` (None, an index, a name or a torch.device)."""
     import torch
 
+    if isinstance(device, torch.device) and device.type == "cuda" and device.index is not None:
+        return torch._C._cuda_getCurrentRawStream(device.index)
     return torch.cuda.current_stream(device).cuda_stream

@@ -166,6 +166,11 @@ class PagedExchange:
         self._store: Pass | None = None
         self._live: dict[int, int] = {}                                   # layer -> slot of the stored chunk
         self._inflight: list[dict[int, int]] = [{} for _ in range(n_layers)]  # layer -> {rank: slot}
+        # per-pass memo of the host work every layer of a pass repeats: the pass whose anchor rotation is in
+        # place, and the pass's clean-list positions of [anchor, working...] (equal on every layer)
+        self._clean_version = 0
+        self._prepared: tuple | None = None
+        self._geometry: tuple | None = None
 
     # ---------------------------------------------------------------- slots
     def slot_pages(self, slot: int) -> list[int]:
@@ -203,6 +208,7 @@ class PagedExchange:
         """``_append_clean_page`` (common.py:110-114) over slots: keep the anchor and the last 7."""
         lst = self.clean[layer]
         lst.append(page)
+        self._clean_version += 1
         if len(lst) > MAX_CLEAN:
             dropped = lst[1:len(lst) - (MAX_CLEAN - 1)]
             lst[:] = lst[:1] + lst[-(MAX_CLEAN - 1):]
@@ -228,6 +234,13 @@ class PagedExchange:
     def prepare_pass(self, p: Pass, height: int, width: int) -> None:
         """Rotate every layer's anchor K to this pass's ``rope_start`` (common.py:70-91) in one launch, unless
         its pages already hold that rotation.  All layers share one clean-list length and geometry."""
+        key = (height, width, self._clean_version)
+        if self._prepared is not None and self._prepared[0] is p and self._prepared[1] == key:
+            return
+        self._prepare_pass(p, height, width)
+        self._prepared = (p, key)
+
+    def _prepare_pass(self, p: Pass, height: int, width: int) -> None:
         if not self.clean[0]:
             return
         if any(len(c) != len(self.clean[0]) for c in self.clean):
@@ -297,7 +310,14 @@ class PagedExchange:
         """(context slots in the reference's order, the pass's own slot) of ``layer``: store
         [anchor, working..., self] or denoise [anchor, working..., live, self, n > r ...]."""
         lst = self.clean[layer]
-        aw = ([lst[0].slot] + [c.slot for c in self._working(layer, p.qf)]) if lst else []
+        geo = self._geometry
+        if geo is None or geo[0] is not p or geo[1] != self._clean_version or len(lst) != geo[3]:
+            n = len(lst)
+            n_work = len(self._working(layer, p.qf)) if n else 0
+            above = inflight_order(p.rank, self._plan.act_ranks)[1:] if p.kind == "denoise" else []
+            geo = self._geometry = (p, self._clean_version, ([0] + list(range(n - n_work, n))) if n else [], n,
+                                    above)
+        aw = [lst[i].slot for i in geo[2]]
         if p.kind == "store":
             own = self._own_slot(layer, p)
             return aw + [own], own
@@ -309,7 +329,7 @@ class PagedExchange:
                 raise RuntimeError(f"[paged] layer {layer}: the store pass has not published this layer "
                                    "(run the store pass first)")
             slots.append(live)
-        above = inflight_order(p.rank, plan.act_ranks)[1:]
+        above = geo[4]
         for n in above:
             if n not in self._inflight[layer]:
                 raise RuntimeError(f"[paged] layer {layer}: rank {n} has not published this layer "

@@ -42,28 +42,39 @@ class PageTable:
         self.pool_pages = pool_pages
         self.dev = torch.tensor(host, dtype=torch.int32, device=device)
 
+    @property
+    def dev_ptr(self) -> int:
+        return self.dev.data_ptr()
+
     def __len__(self) -> int:
         return len(self.host)
 
 
-def _as_thd(x: torch.Tensor, name: str) -> torch.Tensor:
-    """Accept [T, H, D] or the reference's [1, T, H, D] views (paged.py:207-208).
+def _as_thd(x: torch.Tensor, name: str):
+    """Accept [T, H, D] or the reference's [1, T, H, D] views (paged.py:207-208) and return
+    (tensor, address, (T, H, D), token stride) of the data the kernels read.
 
     Heads and head_dim must be dense; the token stride may be larger (e.g. a
     column slice of a fused QKV output) as long as it is a multiple of 8.
+    Anything else is copied dense first.  No view is made on the fast path.
     """
-    if x.dim() == 4:
-        if x.shape[0] != 1:
-            raise ValueError(f"{name}: batch dimension must be 1, got {tuple(x.shape)}")
-        x = x[0]
-    if x.dim() != 3:
-        raise ValueError(f"{name}: expected [T, H, D], got {tuple(x.shape)}")
+    shape = x.shape
+    strides = x.stride()
+    if len(shape) == 4:
+        if shape[0] != 1:
+            raise ValueError(f"{name}: batch dimension must be 1, got {tuple(shape)}")
+        shape, strides = shape[1:], strides[1:]
+    if len(shape) != 3:
+        raise ValueError(f"{name}: expected [T, H, D], got {tuple(shape)}")
     if x.dtype != torch.bfloat16:
         raise ValueError(f"{name}: expected bfloat16, got {x.dtype}")
-    T, H, D = x.shape
-    if x.stride(2) != 1 or x.stride(1) != D or x.stride(0) % 8 or x.data_ptr() % 16 or (T > 1 and x.stride(0) < H * D):
-        x = x.contiguous()
-    return x
+    T, H, D = shape
+    s0, s1, s2 = strides
+    addr = x.data_ptr()
+    if s2 != 1 or s1 != D or s0 % 8 or addr % 16 or (T > 1 and s0 < H * D):
+        x = x.reshape(T, H, D).contiguous()
+        addr, s0 = x.data_ptr(), H * D
+    return x, addr, (T, H, D), (s0 if T > 1 else H * D)
 
 
 def _rope_tables(rope, T: int, D: int, device, tiled: bool = False):
@@ -103,6 +114,12 @@ class Fp8PagePool:
         self.v_codes = torch.zeros(shape_c, dtype=torch.uint8, device=self.device)
         self.k_scales = torch.zeros(shape_s, dtype=torch.float32, device=self.device)
         self.v_scales = torch.zeros(shape_s, dtype=torch.float32, device=self.device)
+        self._cache_ptrs()
+
+    def _cache_ptrs(self) -> None:
+        # device addresses of the four arrays, read by every launch
+        self._k_codes_p, self._v_codes_p = self.k_codes.data_ptr(), self.v_codes.data_ptr()
+        self._k_scales_p, self._v_scales_p = self.k_scales.data_ptr(), self.v_scales.data_ptr()
 
     @classmethod
     def view_of(cls, base: "Fp8PagePool", first_page: int, n_pages: int) -> "Fp8PagePool":
@@ -119,6 +136,7 @@ class Fp8PagePool:
         sl = slice(first_page, first_page + n_pages)
         self.k_codes, self.v_codes = base.k_codes[sl], base.v_codes[sl]
         self.k_scales, self.v_scales = base.k_scales[sl], base.v_scales[sl]
+        self._cache_ptrs()
         return self
 
     @staticmethod
@@ -147,42 +165,30 @@ class Fp8PagePool:
         R rows for any R dividing T and token t uses row t % R (a batch of equal
         chunks, e.g. every layer's anchor, in one launch).
         """
-        k = _as_thd(k, "k")
+        kt, kp, shape, ld = _as_thd(k, "k")
+        vt, vp = None, None
         if v is not None:
-            v = _as_thd(v, "v")
-            if v.shape != k.shape:
-                raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
-        T, H, D = k.shape
+            vt, vp, vshape, vld = _as_thd(v, "v")
+            if vshape != shape:
+                raise ValueError(f"k {tuple(shape)} and v {tuple(vshape)} differ")
+            if vld != ld:
+                # one token stride serves K and V; if they differ, pack from dense copies
+                kt, vt = kt.reshape(shape).contiguous(), vt.reshape(shape).contiguous()
+                kp, vp, ld = kt.data_ptr(), vt.data_ptr(), shape[1] * shape[2]
+        T, H, D = shape
         if H != self.n_heads or D != self.head_dim:
             raise ValueError(f"k has H={H}, D={D}; pool has H={self.n_heads}, D={self.head_dim}")
         if len(table) * self.page_tokens < T:
             raise RuntimeError(f"page table of {len(table)} pages cannot hold {T} tokens")
-        # one token stride serves K and V; if they differ, fall back to dense copies
-        ld = k.stride(0) if T > 1 else H * D
-        if v is not None and (v.stride(0) if T > 1 else H * D) != ld:
-            k, v = k.contiguous(), v.contiguous()
-            ld = H * D
+        pool_args = (table.dev_ptr, len(table), self.page_tokens, self._k_codes_p, self._v_codes_p if vp else None,
+                     self._k_scales_p, self._v_scales_p if vp else None, self.pool_pages,
+                     _lib.stream_handle(self.device))
         if rope is not None:
             cos, sin = _rope_tables(rope, T, D, self.device, tiled)
-            _lib.call(
-                "wf_fp8_kv_pack_rope_tiled",
-                _lib.ptr(k), _lib.ptr(v), T, H, D, ld, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
-                table.dev.data_ptr(), len(table), self.page_tokens,
-                self.k_codes.data_ptr(), self.v_codes.data_ptr() if v is not None else None,
-                self.k_scales.data_ptr(), self.v_scales.data_ptr() if v is not None else None,
-                self.pool_pages,
-                _lib.stream_handle(self.device),
-            )
+            _lib.call("wf_fp8_kv_pack_rope_tiled", kp, vp, T, H, D, ld, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                      *pool_args)
             return
-        _lib.call(
-            "wf_fp8_kv_pack",
-            _lib.ptr(k), _lib.ptr(v), T, H, D, ld,
-            table.dev.data_ptr(), len(table), self.page_tokens,
-            self.k_codes.data_ptr(), self.v_codes.data_ptr() if v is not None else None,
-            self.k_scales.data_ptr(), self.v_scales.data_ptr() if v is not None else None,
-            self.pool_pages,
-            _lib.stream_handle(self.device),
-        )
+        _lib.call("wf_fp8_kv_pack", kp, vp, T, H, D, ld, *pool_args)
 
     def pack_k_norm_rope(self, k: torch.Tensor, v: torch.Tensor | None, table: PageTable, norm_w: torch.Tensor,
                          eps: float, rope: tuple[torch.Tensor, torch.Tensor] | None,
