@@ -13,15 +13,22 @@
  *   - Every pointer is a device pointer unless stated otherwise.  Tensors are
  *     dense row-major; "bf16" buffers hold IEEE bfloat16 bit patterns.
  *   - The library never allocates, frees or caches device memory.  Any
- *     workspace is passed in by the caller.
+ *     workspace is passed in by the caller.  The one exception,
+ *     wf_w8a8_linear_static, keeps its workspace in a fixed static device
+ *     array instead (see its declaration).
  *   - `stream` is a hipStream_t (NULL = the default stream).  Calls only
  *     enqueue work; none of them synchronizes the device.
  *   - Return value: 0 = success, > 0 = a hipError_t from the launch,
  *     < 0 = a WF_E_* argument error.  wf_last_error() returns a
  *     thread-local message describing the last non-zero status.
  *   - Page tables are int32 device arrays of physical page ids.  Entries
- *     outside [0, pool_pages) are skipped by the kernels (never written or
- *     read), and callers are expected to validate them on the host.
+ *     outside [0, pool_pages) are never written or read: the pack skips
+ *     them, the gather-dequant leaves their tokens' output rows untouched,
+ *     and attention
+ *     reads their keys as zero K and zero V -- such a key still takes part
+ *     in the softmax with score 0 (it is not masked like the keys past
+ *     n_kv), so it dilutes the output.  Callers validate tables on the host
+ *     (waveforcing_amd.kv.PageTable does).
  */
 #ifndef WF_API_H
 #define WF_API_H
