@@ -24,11 +24,10 @@
  *   - Page tables are int32 device arrays of physical page ids.  Entries
  *     outside [0, pool_pages) are never written or read: the pack skips
  *     them, the gather-dequant leaves their tokens' output rows untouched,
- *     and attention
- *     reads their keys as zero K and zero V -- such a key still takes part
- *     in the softmax with score 0 (it is not masked like the keys past
- *     n_kv), so it dilutes the output.  Callers validate tables on the host
- *     (waveforcing_amd.kv.PageTable does).
+ *     and attention reads their keys as zero K and zero V -- such a key
+ *     still takes part in the softmax with score 0 (it is not masked like
+ *     the keys past n_kv), so it dilutes the output.  Callers validate
+ *     tables on the host (waveforcing_amd.kv.PageTable does).
  */
 #ifndef WF_API_H
 #define WF_API_H
