@@ -173,6 +173,8 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   const int skey = tid >> 3;
   const int schunk = tid & 7;
   const int HD = p.H * D;
+  const int lane_co = skey * HD + schunk * 16;  // this thread's key row within a page, codes
+  const int lane_so = skey * 4;                 // and scales
 
   __amdgpu_buffer_rsrc_t rk, rv, rsk, rsv;
   if constexpr (DENSE) {
@@ -211,24 +213,34 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
     } else {
       // Branch-free: past n_kv or on an invalid page the offsets are pushed
       // beyond the buffer ranges (>= kOutOfRange > pool size), which read as zero.
+      // The page lookups are uniform across the workgroup, so both pages' base
+      // offsets are scalars; a lane only selects one and adds its own key's
+      // row offset (codes: skey * H * D + h * D + 16 schunk; scales: 4 skey).
       uint32_t lp, rip;
       p.page_div.divmod(static_cast<uint32_t>(t0), lp, rip);
       const int lpi = static_cast<int>(lp), r0 = static_cast<int>(rip);
       const int last = p.n_table - 1;  // >= 0 whenever n_kv > 0
-      int pg0 = p.table[min(lpi, last)];
-      int pg1 = p.table[min(lpi + 1, last)];
+      const int pg0 = p.table[min(lpi, last)];
+      const int pg1 = p.table[min(lpi + 1, last)];
       const bool ok0 = lpi <= last && pg0 >= 0 && pg0 < p.pool_pages;
       const bool ok1 = lpi + 1 <= last && pg1 >= 0 && pg1 < p.pool_pages;
-      pg0 = ok0 ? pg0 : 0;
-      pg1 = ok1 ? pg1 : 0;
       const int split = p.page_tokens - r0;
+      // Keys [0, split) of the tile sit on page pg0 from row r0, keys [split, 64) on pg1 from row 0.
+      // The bases are uint32: cb1 / sb1 wrap below zero when pg1 = 0 and a lane adds at least `split`
+      // rows back; an out-of-range base plus a row offset stays above every buffer range.  Bit masks
+      // rather than conditionals keep the compiler from branching around the multiplies.
+      const uint32_t m0 = 0u - static_cast<uint32_t>(ok0), m1 = 0u - static_cast<uint32_t>(ok1);
+      const int q0 = pg0 & static_cast<int>(m0), q1 = pg1 & static_cast<int>(m1);
+      const uint32_t far0 = static_cast<uint32_t>(kOutOfRange) & ~m0, far1 = static_cast<uint32_t>(kOutOfRange) & ~m1;
+      const uint32_t cb0 = (static_cast<uint32_t>((q0 * p.page_tokens + r0) * HD + h * D) & m0) | far0;
+      const uint32_t cb1 = (static_cast<uint32_t>((q1 * p.page_tokens - split) * HD + h * D) & m1) | far1;
+      const uint32_t sb0 = (static_cast<uint32_t>(((q0 * p.H + h) * p.page_tokens + r0) * 4) & m0) | far0;
+      const uint32_t sb1 = (static_cast<uint32_t>(((q1 * p.H + h) * p.page_tokens - split) * 4) & m1) | far1;
       const bool first = skey < split;
-      const int pg = first ? pg0 : pg1;
-      const int row = first ? r0 + skey : skey - split;
-      const bool ok = (t0 + skey < p.n_kv) && (first ? ok0 : ok1);
-      const uint32_t far = ok ? 0u : static_cast<uint32_t>(kOutOfRange);
-      const uint32_t co = static_cast<uint32_t>(((pg * p.page_tokens + row) * p.H + h) * D + schunk * 16) + far;
-      const uint32_t so = static_cast<uint32_t>(((pg * p.H + h) * p.page_tokens + row) * 4) + far;
+      const uint32_t lm = 0u - static_cast<uint32_t>(skey < p.n_kv - t0);   // all ones for keys before n_kv
+      const uint32_t lfar = static_cast<uint32_t>(kOutOfRange) & ~lm;
+      const uint32_t co = (((first ? cb0 : cb1) + static_cast<uint32_t>(lane_co)) & lm) | lfar;
+      const uint32_t so = (((first ? sb0 : sb1) + static_cast<uint32_t>(lane_so)) & lm) | lfar;
       sk0 = __builtin_amdgcn_raw_buffer_load_b128(rk, static_cast<int>(co), 0, 0);
       sv0 = __builtin_amdgcn_raw_buffer_load_b128(rv, static_cast<int>(co), 0, 0);
       ssk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsk, static_cast<int>(so), 0, 0));
@@ -385,7 +397,6 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
     // P for 16-key step t (keys 16t..16t+15 of the tile): elements 0-3 are
     // keys 4 half + 0..3, elements 4-7 keys 8 + 4 half + 0..3; each step's
     // P feeds its 4 PV MFMAs (O^T += V^T P^T: 4 blocks of 32 d).
-    float ls[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int b = t >> 1, g0 = 2 * (t & 1);
@@ -398,11 +409,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       const uint32_t w0 = cvt_bf16x2(pv[0], pv[1]), w1 = cvt_bf16x2(pv[2], pv[3]);
       const uint32_t w2 = cvt_bf16x2(pv[4], pv[5]), w3 = cvt_bf16x2(pv[6], pv[7]);
       const v8bf pf = __builtin_bit_cast(v8bf, make_uint4(w0, w1, w2, w3));
-      ls[t] = add_bf16x2(w3, add_bf16x2(w2, add_bf16x2(w1, add_bf16x2(w0, 0.f))));
+      l_run = add_bf16x2(w3, add_bf16x2(w2, add_bf16x2(w1, add_bf16x2(w0, l_run))));
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t][db], pf, o[db], 0, 0, 0);
     }
-    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     __syncthreads();
   };
 
