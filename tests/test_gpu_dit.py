@@ -22,7 +22,7 @@ from oracle import kv as okv
 from waveforcing_amd import _lib
 from waveforcing_amd.block import QuantizedWanBlock, random_block_params
 from waveforcing_amd.dit import QuantizedWanDiT, gemm_bf16, random_dit_params
-from waveforcing_amd.exchange import PagedExchange
+from waveforcing_amd.exchange import PagedExchange, tick_plan
 from waveforcing_amd.schedule import FlowMatchSchedule
 from waveforcing_amd.stack import QuantizedWanStack
 
@@ -124,3 +124,38 @@ def test_dit_forward_chunk_matches_oracle(dim, heads, ffn, H, W):
     print(f"text embedding rel L2 {emb_rel:.2e}; x0 rel L2 {rel:.2e}; flow part rel L2 {frel:.2e}")
     assert emb_rel <= 1e-2
     assert frel <= 1e-2
+
+
+def test_dit_concurrent_tick_is_bit_identical():
+    """QuantizedWanDiT.tick(concurrent=True) -- the denoise ranks' patch embedding, layers and head on one
+    stream per rank as a layer wavefront -- returns the same x0, bit for bit, as the sequential tick, over
+    the ticks of a short stream at rf_step 4."""
+    dim, heads, ffn, layers, H, W = 256, 2, 512, 2, 16, 16
+    bparams, dparams, _, ctx = _dit_case(dim, heads, ffn, layers, H, W, seed=31)
+    page = (H // 2) * (W // 2)
+
+    def make():
+        blocks = [QuantizedWanBlock(p, heads, DEV) for p in bparams]
+        dit = QuantizedWanDiT(dparams, QuantizedWanStack(blocks, PagedExchange(layers, heads, page, 3, 21, rf_step=4,
+                                                                                device=DEV)))
+        dit.set_text(ctx.to(DEV))
+        return dit
+
+    seq, con = make(), make()
+    steps = seq.schedule.warp()
+    n_chunks = 6
+    for t in range(n_chunks + 4):
+        plan = tick_plan(t, 4, n_chunks, 3)
+        ins = {}
+        if plan.store_active:
+            ins["store"] = (torch.randn((1, 16, 3, H, W), generator=torch.Generator().manual_seed(t)).to(BF16), 0.0)
+        for r in plan.act_ranks:
+            g = torch.Generator().manual_seed(100 * t + r)
+            ins[r] = (torch.randn((1, 16, 3, H, W), generator=g).to(BF16), steps[r])
+        dev_ins = {k: (x.to(DEV), tt) for k, (x, tt) in ins.items()}
+        a = seq.tick(plan, dev_ins)
+        b = con.tick(tick_plan(t, 4, n_chunks, 3), dev_ins, concurrent=True)
+        torch.cuda.synchronize()
+        assert sorted(a) == sorted(b) == sorted(plan.act_ranks)
+        for r in a:
+            assert torch.equal(a[r], b[r]), f"tick {t} rank {r}"

@@ -186,3 +186,51 @@ def test_stack_tick_releases_slots_when_a_layer_fails():
     with pytest.raises(ValueError, match="5 frames"):
         st.forward_chunk(x.to(DEV), e5, 0, HT, WD, store=False)
     assert all(len(f) == st.exchange.n_slots for f in st.exchange._free)
+
+
+@pytest.mark.parametrize("rf_step,layers", [(2, 2), (4, 3)])
+def test_concurrent_tick_wavefront_is_bit_identical(rf_step, layers):
+    """The denoise ranks of each tick as a layer wavefront on one stream per rank (tick(concurrent=True))
+    give the same hidden states, bit for bit, as the ranks one after another, over a whole stream of ticks
+    (clean list filling, wrapping and slot recycling included), and leave the same clean lists."""
+    params = [random_block_params(DIM, FFN, seed=170 + i) for i in range(layers)]
+    window = 21 if rf_step == 4 else WINDOW
+
+    def make():
+        blocks = [QuantizedWanBlock(p, HEADS, DEV) for p in params]
+        st = QuantizedWanStack(blocks, ex.PagedExchange(layers, HEADS, PAGE, NPB, window, rf_step=rf_step,
+                                                        device=DEV))
+        st.set_text(_text().to(DEV))
+        return st
+
+    seq, con = make(), make()
+    n_chunks = 10
+    for t in range(n_chunks + rf_step):
+        plan = ex.tick_plan(t, rf_step, n_chunks, NPB)
+        keys = (["store"] if plan.store_active else []) + list(plan.act_ranks)
+        ins = {k: _inputs(t, rf_step if k == "store" else k) for k in keys}
+        a = {k: (x.to(DEV), e.to(DEV)) for k, (x, e) in ins.items()}
+        b = {k: (x.to(DEV), e.to(DEV)) for k, (x, e) in ins.items()}
+        seq.tick(plan, a, HT, WD)
+        con.tick(ex.tick_plan(t, rf_step, n_chunks, NPB), b, HT, WD, concurrent=True)
+        torch.cuda.synchronize()
+        for k in keys:
+            assert torch.equal(a[k][0], b[k][0]), f"tick {t} pass {k}"
+        assert [[p.cid for p in c] for c in seq.exchange.clean] == [[p.cid for p in c] for c in con.exchange.clean]
+    for L in range(layers):
+        assert sorted(con.exchange._free[L] + [p.slot for p in con.exchange.clean[L]]) == list(
+            range(con.exchange.n_slots))
+
+
+def test_wavefront_refuses_mixed_or_misordered_passes():
+    st = _stack(_params())
+    plan = ex.tick_plan(RF + 1, RF, 6, NPB)      # store pass + ranks 0 and 1
+    st.exchange.begin_tick(plan)
+    x, e = _inputs(0, 0)
+    x, e = x.to(DEV), e.to(DEV)
+    p1, p0 = st.exchange.denoise_pass(1), st.exchange.denoise_pass(0)
+    with pytest.raises(ValueError, match="highest rank down"):
+        st.run_wavefront([(x, e, p0), (x.clone(), e, p1)], HT, WD)
+    with pytest.raises(ValueError, match="denoise passes"):
+        st.run_wavefront([(x, e, st.exchange.store_pass())], HT, WD)
+    st.exchange.abort_tick()

@@ -226,19 +226,22 @@ class QuantizedWanBlock:
             raise ValueError("only blocks of the same shape and device can share a workspace")
         self._ws = other._ws
 
+    def new_workspace(self, T: int) -> dict:
+        """Activation buffers of one forward over T tokens (any block of this shape can use them)."""
+        dev, dim = self.device, self.dim
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        qbuf = torch.empty((T * max(dim, self.ffn_dim),), dtype=torch.int8, device=dev)
+        return dict(
+            T=T, aq=qbuf[:T * dim].view(T, dim), fq=qbuf[:T * self.ffn_dim].view(T, self.ffn_dim),
+            as_=torch.empty((T,), dtype=torch.float32, device=dev),
+            qkv=torch.empty((T, 3 * dim), **bf), attn=torch.empty((T, dim), **bf), y=torch.empty((T, dim), **bf),
+            cq=torch.empty((T, dim), **bf), ffn=torch.empty((T, self.ffn_dim), **bf),
+        )
+
     def _workspace(self, T: int) -> dict:
         ws = self._ws.get(T)
         if ws is None:
-            dev, dim = self.device, self.dim
-            bf = dict(dtype=torch.bfloat16, device=dev)
-            qbuf = torch.empty((T * max(dim, self.ffn_dim),), dtype=torch.int8, device=dev)
-            ws = dict(
-                aq=qbuf[:T * dim].view(T, dim), fq=qbuf[:T * self.ffn_dim].view(T, self.ffn_dim),
-                as_=torch.empty((T,), dtype=torch.float32, device=dev),
-                qkv=torch.empty((T, 3 * dim), **bf), attn=torch.empty((T, dim), **bf), y=torch.empty((T, dim), **bf),
-                cq=torch.empty((T, dim), **bf), ffn=torch.empty((T, self.ffn_dim), **bf),
-            )
-            self._ws[T] = ws
+            ws = self._ws[T] = self.new_workspace(T)
         return ws
 
     def text_kv(self, context: torch.Tensor):
@@ -258,7 +261,7 @@ class QuantizedWanBlock:
     def forward(self, x: torch.Tensor, e: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pool: Fp8PagePool,
                 context_table: PageTable, own_table: PageTable, n_context: int, text_kv,
                 unroped_k_out: torch.Tensor | None = None, es: torch.Tensor | None = None, pending=None,
-                defer_residual: bool = False):
+                defer_residual: bool = False, ws: dict | None = None):
         """Advance x [T, dim] bf16 in place through the block.
 
         e: [F, 6, dim] bf16 time modulation of the chunk's F frames.
@@ -278,6 +281,9 @@ class QuantizedWanBlock:
         (x, (y, gate)) for the next block (or apply_pending_residual); y is this
         block's workspace, valid until the next forward of a block sharing it
         has run its first LayerNorm.
+        ws: optional activation buffers from :meth:`new_workspace` (passes that run
+        concurrently on different streams each bring their own); default: the
+        block's own, shared with the blocks of its stack.
         """
         T, dim = x.shape
         F = e.shape[0]
@@ -285,7 +291,10 @@ class QuantizedWanBlock:
             raise ValueError(f"{T} tokens do not split into {F} frames")
         ft = T // F
         H, hd = self.heads, self.head_dim
-        ws = self._workspace(T)
+        if ws is None:
+            ws = self._workspace(T)
+        elif ws["T"] != T or ws["qkv"].shape[1] != 3 * dim or ws["ffn"].shape[1] != self.ffn_dim:
+            raise ValueError(f"workspace for {ws['T']} tokens of another shape given to a {T}-token forward")
         # e = (modulation + e).chunk(6)  (causal_model.py:376), bf16: one add; the kernels read
         # the six [F, dim] chunks as strided frame rows of it.
         if es is None:

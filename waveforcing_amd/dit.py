@@ -176,14 +176,51 @@ class QuantizedWanDiT:
             hit = self._time[key] = (e, e0)
         return hit
 
-    def _workspace(self, T: int) -> dict:
-        ws = self._ws.get(T)
+    def _workspace(self, T: int, slot: int = 0) -> dict:
+        """Buffers of one pass over T tokens; concurrent passes use different slots."""
+        ws = self._ws.get((T, slot))
         if ws is None:
             bf = dict(dtype=torch.bfloat16, device=self.device)
             ws = dict(patches=torch.empty((T, IN_DIM * 4), **bf), x=torch.empty((T, self.dim), **bf),
                       h=torch.empty((T, self.dim), **bf), flow=torch.empty((T, OUT_DIM * 4), **bf))
-            self._ws[T] = ws
+            self._ws[(T, slot)] = ws
         return ws
+
+    @staticmethod
+    def _check_latent(noisy: torch.Tensor) -> torch.Tensor:
+        if noisy.dim() != 5 or noisy.shape[0] != 1 or noisy.shape[1] != IN_DIM or noisy.dtype != torch.bfloat16:
+            raise ValueError(f"noisy must be bf16 [1, {IN_DIM}, F, H, W], got {tuple(noisy.shape)} {noisy.dtype}")
+        return noisy.contiguous()
+
+    def _embed(self, noisy: torch.Tensor, ws: dict) -> torch.Tensor:
+        """Patch gather + patch embedding of a checked latent into ws["x"]."""
+        _, C, Fr, H, W = noisy.shape
+        _lib.call("wf_patchify_bf16", noisy.data_ptr(), 1, C, Fr, H, W, ws["patches"].data_ptr(),
+                  _lib.stream_handle(self.device))
+        return gemm_bf16(ws["patches"], self.patch_w, self.patch_b, out=ws["x"])
+
+    def _head(self, x: torch.Tensor, e: torch.Tensor, noisy: torch.Tensor, t: float, ws: dict,
+              x0: torch.Tensor) -> torch.Tensor:
+        """Head (modulated LayerNorm, Linear(dim, 64)), unpatchify and x0 = xt - sigma * flow into x0."""
+        _, C, Fr, H, W = noisy.shape
+        T = x.shape[0]
+        st = _lib.stream_handle(self.device)
+        # head: LayerNorm + (shift, scale) = head modulation + e per frame, then Linear(dim, 64)
+        es = self.head_mod[0].unsqueeze(0) + e.unsqueeze(1)          # [F, 2, dim] bf16
+        _lib.call("wf_ln_modulate_quant", x.data_ptr(), T, self.dim, x.stride(0), EPS, None, None,
+                  es[:, 0].data_ptr(), es[:, 1].data_ptr(), es.stride(0), T // Fr, ws["h"].data_ptr(),
+                  ws["h"].stride(0), None, None, st)
+        flow = gemm_bf16(ws["h"], self.head_w, self.head_b, out=ws["flow"])
+        _lib.call("wf_unpatchify_flow_x0_bf16", flow.data_ptr(), noisy.data_ptr(), 1, C, Fr, H, W,
+                  self.schedule.sigma_x0(t), x0.data_ptr(), st)
+        return x0
+
+    def _x0_buffer(self, noisy: torch.Tensor, x0_out: torch.Tensor | None) -> torch.Tensor:
+        _, C, Fr, H, W = noisy.shape
+        x0 = x0_out if x0_out is not None else torch.empty((1, Fr, C, H, W), dtype=torch.bfloat16, device=self.device)
+        if tuple(x0.shape) != (1, Fr, C, H, W) or not x0.is_contiguous() or x0.dtype != torch.bfloat16:
+            raise ValueError(f"x0_out must be contiguous bf16 [1, {Fr}, {C}, {H}, {W}]")
+        return x0
 
     # -- one pass of a tick
     def run_pass(self, noisy: torch.Tensor, t: float, p: Pass, x0_out: torch.Tensor | None = None,
@@ -191,38 +228,23 @@ class QuantizedWanDiT:
         """The forward of noisy [1, 16, F, H, W] bf16 (B, C, T, H, W) at timestep t as pass p of the current tick;
         returns x0 [1, F, 16, H, W] bf16 (B, T, C, H, W), or None with ``want_x0=False`` (a store pass,
         whose x0 the wavefront drops: engine.py:383-389)."""
-        if noisy.dim() != 5 or noisy.shape[0] != 1 or noisy.shape[1] != IN_DIM or noisy.dtype != torch.bfloat16:
-            raise ValueError(f"noisy must be bf16 [1, {IN_DIM}, F, H, W], got {tuple(noisy.shape)} {noisy.dtype}")
-        noisy = noisy.contiguous()
+        noisy = self._check_latent(noisy)
         _, C, Fr, H, W = noisy.shape
         hp, wp = H // 2, W // 2
-        T = Fr * hp * wp
-        ws = self._workspace(T)
-        st = _lib.stream_handle(self.device)
-        _lib.call("wf_patchify_bf16", noisy.data_ptr(), 1, C, Fr, H, W, ws["patches"].data_ptr(), st)
-        x = gemm_bf16(ws["patches"], self.patch_w, self.patch_b, out=ws["x"])
+        ws = self._workspace(Fr * hp * wp)
+        x = self._embed(noisy, ws)
         e, e0 = self.time_modulation(t, Fr)
         self.stack.run_pass(x, e0, p, hp, wp)
         if not want_x0:
             return None
-        # head: LayerNorm + (shift, scale) = head modulation + e per frame, then Linear(dim, 64)
-        es = self.head_mod[0].unsqueeze(0) + e.unsqueeze(1)          # [F, 2, dim] bf16
-        _lib.call("wf_ln_modulate_quant", x.data_ptr(), T, self.dim, x.stride(0), EPS, None, None,
-                  es[:, 0].data_ptr(), es[:, 1].data_ptr(), es.stride(0), T // Fr, ws["h"].data_ptr(),
-                  ws["h"].stride(0), None, None, st)
-        flow = gemm_bf16(ws["h"], self.head_w, self.head_b, out=ws["flow"])
-        x0 = x0_out if x0_out is not None else torch.empty((1, Fr, C, H, W), dtype=torch.bfloat16, device=self.device)
-        if tuple(x0.shape) != (1, Fr, C, H, W) or not x0.is_contiguous() or x0.dtype != torch.bfloat16:
-            raise ValueError(f"x0_out must be contiguous bf16 [1, {Fr}, {C}, {H}, {W}]")
-        _lib.call("wf_unpatchify_flow_x0_bf16", flow.data_ptr(), noisy.data_ptr(), 1, C, Fr, H, W,
-                  self.schedule.sigma_x0(t), x0.data_ptr(), st)
-        return x0
+        return self._head(x, e, noisy, t, ws, self._x0_buffer(noisy, x0_out))
 
-    def tick(self, plan: TickPlan, inputs: dict) -> dict:
+    def tick(self, plan: TickPlan, inputs: dict, concurrent: bool = False) -> dict:
         """One wavefront tick on this GPU: ``inputs`` maps "store" (when the store rank is active) and each
         active denoise rank to (noisy [1, 16, F, H, W], timestep); the store pass runs first, then the ranks
-        from the highest down (the order the reference's flag waits impose); returns {rank: x0} of the
-        denoise passes (the store pass's x0 is dropped, as the reference drops it)."""
+        from the highest down (the order the reference's flag waits impose), one after another or
+        (``concurrent``) as a layer wavefront on one stream per rank, with bit-identical results; returns
+        {rank: x0} of the denoise passes (the store pass's x0 is dropped, as the reference drops it)."""
         ex = self.stack.exchange
         ex.begin_tick(plan)
         out = {}
@@ -230,14 +252,43 @@ class QuantizedWanDiT:
             if plan.store_active:
                 noisy, t = inputs["store"]
                 self.run_pass(noisy, t, ex.store_pass(), want_x0=False)
-            for r in sorted(plan.act_ranks, reverse=True):
-                noisy, t = inputs[r]
-                out[r] = self.run_pass(noisy, t, ex.denoise_pass(r))
+            ranks = sorted(plan.act_ranks, reverse=True)
+            if concurrent and len(ranks) > 1:
+                out = self._denoise_wavefront(ranks, inputs, [ex.denoise_pass(r) for r in ranks])
+            else:
+                for r in ranks:
+                    noisy, t = inputs[r]
+                    out[r] = self.run_pass(noisy, t, ex.denoise_pass(r))
         except BaseException:
             ex.abort_tick()
             raise
         ex.end_tick()
         return out
+
+    def _denoise_wavefront(self, ranks: list, inputs: dict, passes: list) -> dict:
+        """The denoise passes of a tick as a layer wavefront (QuantizedWanStack.run_wavefront), each rank's
+        patch embedding before and head after its layers on the rank's stream."""
+        lat = [self._check_latent(inputs[r][0]) for r in ranks]
+        ts = [inputs[r][1] for r in ranks]
+        shapes = {tuple(n.shape) for n in lat}
+        if len(shapes) != 1:
+            raise ValueError(f"the ranks' latents differ in shape: {sorted(shapes)}")
+        _, C, Fr, H, W = lat[0].shape
+        hp, wp = H // 2, W // 2
+        T = Fr * hp * wp
+        wss = [self._workspace(T, slot=i) for i in range(len(ranks))]
+        mods = [self.time_modulation(t, Fr) for t in ts]
+        x0s = [self._x0_buffer(n, None) for n in lat]
+
+        def pre(i):
+            self._embed(lat[i], wss[i])
+
+        def post(i):
+            self._head(wss[i]["x"], mods[i][0], lat[i], ts[i], wss[i], x0s[i])
+
+        self.stack.run_wavefront([(wss[i]["x"], mods[i][1], p) for i, p in enumerate(passes)],
+                                 hp, wp, pre=pre, post=post)
+        return dict(zip(ranks, x0s))
 
     def forward_chunk(self, noisy: torch.Tensor, t: float, chunk: int, store: bool = False):
         """One chunk alone as a tick of its own (backend.py:456-490's call for a single chunk): a store pass

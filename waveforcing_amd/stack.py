@@ -9,8 +9,16 @@ packs its own K/V into its chunk's slot straight from the QKV projection
 for the pass (anchor, working set, live and in-flight chunks).
 
 A tick of the wavefront (wave_rt/denoiser/engine.py:300-420) runs the store
-rank's pass and every active denoise rank's pass on this GPU one after
-another (:meth:`QuantizedWanStack.tick`).  The stack works on hidden states:
+rank's pass and every active denoise rank's pass on this GPU
+(:meth:`QuantizedWanStack.tick`): the store pass first, then the denoise
+ranks, either one after another or, with ``concurrent=True``, as a layer
+wavefront on one HIP stream per rank.  Rank r's layer L needs only layer L of
+the ranks above it (their in-flight chunks), the dependency the reference's
+per-layer flag waits express between GPUs (paged.py:147-154), so on one GPU
+each rank's stream waits for an event the next rank up records after its
+layer L; the ranks' kernels then fill the CUs and launch gaps a single pass
+leaves idle.  Every rank brings its own activation buffers, and all of them
+share the anchor rotation of the tick's denoise geometry.  The stack works on hidden states:
 the DiT's embeddings and output head around it live in
 waveforcing_amd.dit, so the caller hands in each pass's hidden states
 x [T, dim], its time modulation e [F, 6, dim] and the text context.
@@ -75,18 +83,106 @@ class QuantizedWanStack:
         apply_pending_residual(x, pending, x.shape[0] // e.shape[0])
         return x
 
-    def tick(self, plan: TickPlan, inputs: dict, height: int, width: int) -> TickPlan:
+    # -- concurrent denoise passes
+    def side_streams(self, n: int) -> list:
+        """n HIP streams of this stack's device (default priority), created once and reused."""
+        dev = self.blocks[0].device
+        have = getattr(self, "_streams", [])
+        while len(have) < n:
+            have.append(torch.cuda.Stream(device=dev))
+        self._streams = have
+        return have[:n]
+
+    def pass_workspaces(self, n: int, T: int) -> list:
+        """Activation buffers for n concurrent passes of T tokens (created once per (slot, T))."""
+        cache = getattr(self, "_pass_ws", {})
+        self._pass_ws = cache
+        out = []
+        for i in range(n):
+            ws = cache.get((i, T))
+            if ws is None:
+                ws = cache[(i, T)] = self.blocks[0].new_workspace(T)
+            out.append(ws)
+        return out
+
+    def run_wavefront(self, items: list, height: int, width: int, pre=None, post=None) -> None:
+        """Advance each (x, e, pass) of ``items`` -- denoise passes of the current tick, ordered from the highest
+        rank down -- in place through every layer, pass i on its own stream, as a wavefront over the layers: pass
+        i's layer L waits for pass i - 1's layer L.  The anchor rotation of their common geometry, the RoPE
+        tables and the modulation sums are prepared on the current stream first; ``pre(i)`` / ``post(i)``, if
+        given, enqueue work of pass i on its stream before its first / after its last layer.  Returns with the
+        current stream waiting for every pass."""
+        if self.text_kv is None:
+            raise RuntimeError("set_text() first")
+        passes = [p for _, _, p in items]
+        if any(p.kind != "denoise" for p in passes) or len({(p.csf, p.qf) for p in passes}) > 1:
+            raise ValueError("a wavefront runs the denoise passes of one tick (one context geometry)")
+        ranks = [p.rank for p in passes]
+        if ranks != sorted(ranks, reverse=True) or len(set(ranks)) != len(ranks):
+            raise ValueError(f"wavefront passes must run from the highest rank down, got ranks {ranks}")
+        ex = self.exchange
+        n = len(items)
+        dev = self.blocks[0].device
+        T = items[0][0].shape[0]
+        ex.prepare_pass(passes[0], height, width)
+        wss = self.pass_workspaces(n, T)
+        state = []
+        for x, e, p in items:
+            cos, sin = rope.cos_sin(ex.npb, height, width, p.chunk * ex.npb, ex.head_dim, device=x.device)
+            state.append([x, None, cos, sin, self._modulation.unsqueeze(1) + e.unsqueeze(0)])
+        evs = getattr(self, "_events", [])
+        while len(evs) < n:
+            evs.append([torch.cuda.Event() for _ in self.blocks])
+        self._events = evs
+        cur = torch.cuda.current_stream(dev)
+        streams = self.side_streams(n)
+        try:
+            for i, st in enumerate(streams):
+                st.wait_stream(cur)
+                if pre is not None:
+                    with torch.cuda.stream(st):
+                        pre(i)
+            for L, blk in enumerate(self.blocks):
+                for i, (_, e, p) in enumerate(items):
+                    st = streams[i]
+                    with torch.cuda.stream(st):
+                        if i > 0:
+                            st.wait_event(evs[i - 1][L])
+                        x, pending, cos, sin, es_all = state[i]
+                        pool, ctx, own, n_ctx = ex.layer_context(L, p, height, width)
+                        x, pending = blk.forward(x, e, cos, sin, pool, ctx, own, n_ctx, self.text_kv[L],
+                                                 es=es_all[L], pending=pending, defer_residual=True, ws=wss[i])
+                        state[i][0], state[i][1] = x, pending
+                        if i + 1 < n:
+                            evs[i][L].record(st)
+            for i, (x, e, p) in enumerate(items):
+                with torch.cuda.stream(streams[i]):
+                    apply_pending_residual(state[i][0], state[i][1], x.shape[0] // e.shape[0])
+                    if post is not None:
+                        post(i)
+        finally:
+            # whatever was enqueued completes before the current stream goes on (and before the tables above,
+            # allocated on it, can be reused)
+            for st in streams:
+                cur.wait_stream(st)
+
+    def tick(self, plan: TickPlan, inputs: dict, height: int, width: int, concurrent: bool = False) -> TickPlan:
         """One wavefront tick on this GPU: ``inputs`` maps "store" (when the store rank is active) and each
         active denoise rank to its (x, e); the store pass runs first, then the ranks from the highest down,
-        each x advanced in place; the stored chunk joins the clean lists at the end.  On an error the
-        tick's slots are returned and nothing is promoted."""
+        each x advanced in place, one after another or (``concurrent``) as a layer wavefront on one stream
+        per rank (bit-identical results); the stored chunk joins the clean lists at the end.  On an error
+        the tick's slots are returned and nothing is promoted."""
         ex = self.exchange
         ex.begin_tick(plan)
         try:
             if plan.store_active:
                 self.run_pass(*inputs["store"], ex.store_pass(), height, width)
-            for r in sorted(plan.act_ranks, reverse=True):
-                self.run_pass(*inputs[r], ex.denoise_pass(r), height, width)
+            ranks = sorted(plan.act_ranks, reverse=True)
+            if concurrent and len(ranks) > 1:
+                self.run_wavefront([(*inputs[r], ex.denoise_pass(r)) for r in ranks], height, width)
+            else:
+                for r in ranks:
+                    self.run_pass(*inputs[r], ex.denoise_pass(r), height, width)
         except BaseException:
             ex.abort_tick()
             raise
