@@ -298,7 +298,7 @@ def bench_exchange(steps: int, warmup: int, dev: str):
             "gbs": tick_bytes / (ms * 1e-3) / 1e9, "rank0_context_keys": n_ctx[-1]}
 
 
-def bench_stack(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
+def bench_stack(steps: int, warmup: int, dev: str, preset: str = "1.3b", ticks_only: bool = False):
     """A steady-state wavefront tick of all the Wan blocks of a preset (30 for 1.3B, 40 for 14B) on one GPU:
     rf_step 4, 21-frame window, 3-frame chunks of 4680 tokens (30x52 grid), 512-token text context.  8 store
     passes through the stack fill the clean list (anchor + 7); the timed tick is tick 12: the store pass of
@@ -347,6 +347,11 @@ def bench_stack(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
             ex.abort_tick()
 
     ms_tick_con = _timed(tick_concurrent, max(2, steps // 3), 1)
+    if ticks_only:
+        out = {"ms_per_tick_5_passes": ms_tick, "ms_per_tick_5_passes_concurrent": ms_tick_con}
+        del st, xs, x0
+        torch.cuda.empty_cache()
+        return out
     # rank 0's pass alone, inside an open tick whose other passes have run
     ex.begin_tick(plan)
     for key in ("store", 3, 2, 1):
@@ -570,7 +575,7 @@ def main() -> None:
                     help="minimum untimed warm-up of the KV workloads (profiler runs use 0)")
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
-                                       "copy"],
+                                       "tick_1p3b", "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -589,7 +594,7 @@ def main() -> None:
               "block_1p3b": lambda s, w, d: bench_block("1.3b", s, w, d),
               "block_14b": lambda s, w, d: bench_block("14b", s, w, d), "exchange_1p3b": bench_exchange,
               "stack_1p3b": bench_stack, "stack_14b": lambda s, w, d: bench_stack(s, w, d, "14b"),
-              "dit_1p3b": bench_dit,
+              "dit_1p3b": bench_dit, "tick_1p3b": lambda s, w, d: bench_stack(s, w, d, ticks_only=True),
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return

@@ -47,6 +47,10 @@ class QuantizedWanStack:
         # every layer's modulation table, so one add per pass forms all the ``modulation + e``
         self._modulation = torch.stack([b.modulation[0] for b in blocks])   # [L, 6, dim]
         self.text_kv: list | None = None
+        # the layer wavefront's streams, per-layer events and per-pass activation buffers (created on first use)
+        self._streams: list = []
+        self._events: list = []
+        self._pass_ws: dict = {}
 
     @classmethod
     def random(cls, preset: str = "1.3b", n_layers: int | None = None, seed: int = 0, device="cuda",
@@ -87,21 +91,17 @@ class QuantizedWanStack:
     def side_streams(self, n: int) -> list:
         """n HIP streams of this stack's device (default priority), created once and reused."""
         dev = self.blocks[0].device
-        have = getattr(self, "_streams", [])
-        while len(have) < n:
-            have.append(torch.cuda.Stream(device=dev))
-        self._streams = have
-        return have[:n]
+        while len(self._streams) < n:
+            self._streams.append(torch.cuda.Stream(device=dev))
+        return self._streams[:n]
 
     def pass_workspaces(self, n: int, T: int) -> list:
         """Activation buffers for n concurrent passes of T tokens (created once per (slot, T))."""
-        cache = getattr(self, "_pass_ws", {})
-        self._pass_ws = cache
         out = []
         for i in range(n):
-            ws = cache.get((i, T))
+            ws = self._pass_ws.get((i, T))
             if ws is None:
-                ws = cache[(i, T)] = self.blocks[0].new_workspace(T)
+                ws = self._pass_ws[(i, T)] = self.blocks[0].new_workspace(T)
             out.append(ws)
         return out
 
@@ -130,10 +130,9 @@ class QuantizedWanStack:
         for x, e, p in items:
             cos, sin = rope.cos_sin(ex.npb, height, width, p.chunk * ex.npb, ex.head_dim, device=x.device)
             state.append([x, None, cos, sin, self._modulation.unsqueeze(1) + e.unsqueeze(0)])
-        evs = getattr(self, "_events", [])
+        evs = self._events
         while len(evs) < n:
             evs.append([torch.cuda.Event() for _ in self.blocks])
-        self._events = evs
         cur = torch.cuda.current_stream(dev)
         streams = self.side_streams(n)
         try:
