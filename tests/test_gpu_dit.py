@@ -159,3 +159,45 @@ def test_dit_concurrent_tick_is_bit_identical():
         assert sorted(a) == sorted(b) == sorted(plan.act_ranks)
         for r in a:
             assert torch.equal(a[r], b[r]), f"tick {t} rank {r}"
+
+
+def test_wavefront_generate_sequential_and_concurrent_agree():
+    """WavefrontDenoiser.generate over 5 chunks at rf_step 4 (the loop of engine.py:289-560 on one GPU):
+    the sequential and the concurrent tick give the same clean latents, bit for bit; chunk 0 -- which has
+    no older chunk to attend to -- equals its trajectory replayed alone on a fresh DiT (rank 0's pass at each
+    DMD step through forward_chunk, re-noised between steps with seed 1000 * 0 + stage)."""
+    from waveforcing_amd.schedule import det_renoise
+    from waveforcing_amd.wavefront import WavefrontDenoiser
+
+    dim, heads, ffn, layers, H, W = 256, 2, 512, 2, 16, 16
+    bparams, dparams, _, ctx = _dit_case(dim, heads, ffn, layers, H, W, seed=41)
+    page = (H // 2) * (W // 2)
+
+    def make():
+        blocks = [QuantizedWanBlock(p, heads, DEV) for p in bparams]
+        dit = QuantizedWanDiT(dparams, QuantizedWanStack(blocks, PagedExchange(layers, heads, page, 3, 21, rf_step=4,
+                                                                                device=DEV)))
+        dit.set_text(ctx.to(DEV))
+        return dit
+
+    n_chunks = 5
+    noise = torch.randn((1, 16, 3 * n_chunks, H, W), generator=torch.Generator().manual_seed(42)).to(BF16).to(DEV)
+    done = []
+    seq_dit = make()
+    seq = WavefrontDenoiser(seq_dit).generate(noise, on_chunk=lambda c, lat: done.append(c))
+    con = WavefrontDenoiser(make()).generate(noise, concurrent=True)
+    torch.cuda.synchronize()
+    assert done == list(range(n_chunks))
+    assert torch.isfinite(seq.float()).all()
+    assert torch.equal(seq, con)
+    # every chunk's store pass added one clean page per layer
+    assert all(len(c) == n_chunks for c in seq_dit.stack.exchange.clean)
+
+    alone = make()
+    dsl = alone.schedule.warp()
+    lat = noise[:, :, 0:3].contiguous()
+    for r in range(4):
+        x0 = alone.forward_chunk(lat, dsl[r], chunk=0).permute(0, 2, 1, 3, 4).contiguous()
+        lat = det_renoise(x0, dsl[r + 1], 0, r, alone.schedule) if r < 3 else x0
+    torch.cuda.synchronize()
+    assert torch.equal(seq[:, :, 0:3], lat)
