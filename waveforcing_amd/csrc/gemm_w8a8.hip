@@ -25,6 +25,9 @@
 //    r at 16 (c ^ ((r/2)%8)) and the 16-byte fragment reads of 16 consecutive
 //    rows hit 16 distinct bank groups.  The buffer descriptor's range
 //    zero-fills rows past M / N, and K-tail chunks are pointed past it.
+//  * Prologue: the waves that win the issue arbitration of their SIMD (0..3)
+//    fetch all of stage 0, their SIMD mates stage 1, so the first stage is
+//    not queued behind the second.
 //  * Three LDS stages of 48 KB.  A K step (128 bytes) is SUB sub-steps of one
 //    MFMA depth (4 x 32 bytes for int8, 2 x 64 for e4m3); fragments of
 //    sub-step g+1 are read while the MFMAs of g issue, the reads and DMAs
@@ -35,9 +38,14 @@
 //    sub-step's MFMAs cover the first reads of the next stage; the DMA of
 //    step j is spread over the last sub-step of step j-3 and the first SUB-1
 //    of step j-2.
-//  * Epilogue: scales and bias are loaded at kernel start; results are
-//    converted with v_cvt_pk_bf16_f32 (round to nearest even), staged in LDS
-//    and written as row-contiguous 16-byte vectors (full 128-byte lines).
+//    The last three steps are peeled so that no step past K is fetched.
+//  * Epilogue: the row scales are loaded at kernel start, the tile's column
+//    scales and bias reach LDS by DMA (three instructions, not a copy per
+//    lane, which would queue ~100 KB per CU ahead of the first stage);
+//    results are converted with v_cvt_pk_bf16_f32 (round to nearest even);
+//    each wave stages 32-row slabs of its 64 x 64 sub-tile in its own LDS
+//    area and stores them as full 128-byte row segments while it converts
+//    the next slab.
 //  * Tiles are ordered so that the workgroups one XCD receives (blockIdx % 8)
 //    form a contiguous range, walked in bands of 8 tile rows, so co-resident
 //    workgroups share A and W panels in that XCD's L2.
@@ -72,6 +80,12 @@ constexpr int NUM_XCD = 8;
 constexpr int OUT_PITCH = BN * 2 + 16;  // bf16 epilogue tile row pitch (bytes)
 static_assert(NBA * 8 * NW == BM && NBB * 8 * NW == BN, "DMA blocks");
 static_assert(BM * OUT_PITCH <= ST * STAGE, "epilogue tile fits the stages");
+// The one-round kernel's per-column epilogue operands in LDS, past the stages: sw (fp32) at 0, the bias
+// as it arrives (bf16) at 1024 and converted to fp32 at 2048.
+constexpr int EPI_BYTES = 3072;
+// Per-wave output staging of the one-round kernel: two 32-row slabs of the wave's 64 x 64 sub-tile.
+constexpr int WPITCH = BN / WN * 2 + 16;
+static_assert(NW * 2 * 32 * WPITCH <= ST * STAGE, "wave staging fits the stages");
 // Word 3 of a raw (untyped, stride 0) buffer resource on gfx9-family parts:
 // DATA_FORMAT = 32 bit.  With it, offsets >= num_records read as zero.
 constexpr int kBufferRsrcWord3 = 0x00020000;
@@ -121,6 +135,10 @@ __device__ inline void wait_counts() {
 __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds_block, int offset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_block, 16, offset, 0, 0, 0);
 }
+__device__ inline void dma4(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds_block, int offset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds_block, 4, offset, 0, 0, 0);
+}
+
 
 struct GemmArgs {
   const void* a;         // [M, K] int8 or e4m3
@@ -135,14 +153,34 @@ struct GemmArgs {
   int vec16;             // y and ldy allow 16-byte row stores
 };
 
-template <typename OP, bool HAS_BIAS, bool GELU>
+// The epilogue operands of the 256 columns from n0 into epi: sw by wave 0 (one 1 KB DMA), bias by wave 1
+// (two 256-byte DMAs).  Columns past N read as zero (N % 4 == 0, so no access straddles the end).
+template <bool SW, bool BIAS>
+__device__ inline void epi_dma(const GemmArgs& p, int wave, int lane, int n0, uint8_t* epi) {
+  if constexpr (SW) {
+    if (wave == 0)
+      dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.sw), 0, p.N * 4, kBufferRsrcWord3), epi,
+            (n0 + 4 * lane) * 4);
+  }
+  if constexpr (BIAS) {
+    if (wave == 1) {
+      const __amdgpu_buffer_rsrc_t rb =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.bias), 0, p.N * 2, kBufferRsrcWord3);
+      dma4(rb, epi + 1024, (n0 + 2 * lane) * 2);
+      dma4(rb, epi + 1280, (n0 + 128 + 2 * lane) * 2);
+    }
+  }
+}
+
+template <typename OP, bool HAS_BIAS, bool GELU, bool ACC>
 __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   constexpr bool kI8 = std::is_same<OP, OpI8>::value;
   constexpr int SUB = OP::SUB;
   constexpr int PIECES = OP::PIECES;
   constexpr int CPS = BK / 16 / SUB;  // 16-byte K chunks per sub-step (2 per lane pair)
   static_assert(CPS == 2 * PIECES, "sub-step geometry");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[ST * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[ST * STAGE + EPI_BYTES];
+  uint8_t* const epi = lds + ST * STAGE;
 
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (p.N + BN - 1) / BN;
@@ -164,10 +202,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
-  // Epilogue operands, loaded now so their latency hides under the K loop.
+  // Epilogue operands: the row scales now (their latency hides under the K loop), the per-column sw and
+  // bias by DMA into LDS ahead of the stages (three instructions instead of a per-lane copy each).
   float sxv[MI];
-  float4 swv[NI][4];
-  uint2 bv[NI][4];
   float scale = 0.f;
   if constexpr (kI8) {
 #pragma unroll
@@ -175,14 +212,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   } else {
     scale = p.sx[0] * p.sw[0];
   }
-#pragma unroll
-  for (int j = 0; j < NI; ++j)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int gn = min(n0 + wn * (BN / WN) + j * 32 + 8 * g + 4 * half, p.N - 4);
-      if constexpr (kI8) swv[j][g] = *reinterpret_cast<const float4*>(p.sw + gn);
-      bv[j][g] = HAS_BIAS ? *reinterpret_cast<const uint2*>(p.bias + gn) : make_uint2(0, 0);
-    }
+  epi_dma<kI8, HAS_BIAS>(p, wave, lane, n0, epi);
 
   const __amdgpu_buffer_rsrc_t rsrc_a =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), 0, p.M * p.K, kBufferRsrcWord3);
@@ -207,6 +237,16 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
       dma16(rsrc_a, lds + stage * STAGE + (j * NW + wave) * 1024, off);
     else
       dma16(rsrc_w, lds + stage * STAGE + A_BYTES + ((j - NBA) * NW + wave) * 1024, off);
+  };
+  // Block j of wave w (w = wave +- NW/2): its rows are this wave's plus (w - wave) * 8, with the same
+  // swizzled chunk (the row difference is a multiple of 16).
+  auto dma_of = [&](auto J, int k0, int stage, int w) {
+    constexpr int j = decltype(J)::value;
+    const int off = (k0 + dcol[j] < p.K) ? doff[j] + (w - wave) * 8 * p.K + k0 : kOutOfRange;
+    if constexpr (j < NBA)
+      dma16(rsrc_a, lds + stage * STAGE + (j * NW + w) * 1024, off);
+    else
+      dma16(rsrc_w, lds + stage * STAGE + A_BYTES + ((j - NBA) * NW + w) * 1024, off);
   };
 
   // Fragment pieces: sub-step s, lane half h, piece e is K chunk
@@ -241,12 +281,14 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   // The MFMAs of buffer B with, spread between them, the reads of sub-step rs
   // of rstage into buffer 1-B and DMA slot SLOT (of SUB per step) for the
   // step at K offset dk0 into dstage.
-  auto substep = [&](auto B, int rstage, int rs, auto SLOT, int dk0, int dstage) {
+  // RD / DM switch the reads and the DMAs off (the last steps have no next sub-step or step to fetch).
+  auto substep = [&](auto B, int rstage, int rs, auto SLOT, int dk0, int dstage, auto RD, auto DM) {
     constexpr int b = decltype(B)::value;
     constexpr int slot = decltype(SLOT)::value;
+    constexpr bool rd = decltype(RD)::value, dm = decltype(DM)::value;
     constexpr int d_lo = (slot * NDMA + SUB - 1) / SUB;
-    constexpr int d_hi = ((slot + 1) * NDMA + SUB - 1) / SUB;
-    constexpr int NMF = MI * NI, NRD = (MI + NI) * PIECES;
+    constexpr int d_hi = dm ? ((slot + 1) * NDMA + SUB - 1) / SUB : d_lo;
+    constexpr int NMF = MI * NI, NRD = rd ? (MI + NI) * PIECES : 0;
     constexpr int NOPS = NRD + d_hi - d_lo;
     static_for<NMF>([&](auto Q) {
       constexpr int q = decltype(Q)::value;
@@ -267,51 +309,97 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   // Steps past K load zeros (a zero contribution): every step runs the same
   // code, and the last DMAs (of steps nk .. nk+2) only fill unused stages.
   const int nk = (p.K + BK - 1) / BK;
-  static_for<NDMA>([&](auto J) { dma(J, 0, 0); });
-  static_for<NDMA>([&](auto J) { dma(J, BK, 1); });
-  wait_counts<NDMA, 0>();
+  // Prologue: waves 0..NW/2-1, which win the issue arbitration of the SIMD they share with wave + NW/2,
+  // fetch all of stage 0 (their blocks and their SIMD mate's); the mates fetch stage 1.  So stage 0 is
+  // not queued behind stage 1, and only stage 0 is waited for here (the mates' stage-1 DMAs are older
+  // than the NDMA most recent ones at the first step's wait, which therefore covers them).
+  if (wave < NW / 2) {
+    static_for<NDMA>([&](auto J) {
+      dma_of(J, 0, 0, wave);
+      dma_of(J, 0, 0, wave + NW / 2);
+    });
+    wait_counts<0, 0>();
+  } else {
+    static_for<NDMA>([&](auto J) {
+      dma_of(J, BK, 1, wave);
+      dma_of(J, BK, 1, wave - NW / 2);
+    });
+  }
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  static_for<(NDMA + SUB - 1) / SUB>([&](auto J) { dma(J, 2 * BK, 2); });
+  // the bias as fp32 for the epilogue (published by the first K step's barrier)
+  if constexpr (HAS_BIAS) {
+    if (wave == 1) {
+      const uint2 b = *reinterpret_cast<const uint2*>(epi + 1024 + lane * 8);
+      *reinterpret_cast<float4*>(epi + 2048 + lane * 16) =
+          make_float4(__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u), __uint_as_float(b.y << 16),
+                      __uint_as_float(b.y & 0xffff0000u));
+    }
+  }
+  if (nk >= 3) static_for<(NDMA + SUB - 1) / SUB>([&](auto J) { dma(J, 2 * BK, 2); });
   static_for<(MI + NI) * PIECES>([&](auto O) { frag_read(O, ic<0>{}, 0, 0); });
   __builtin_amdgcn_sched_barrier(0);
 
+  // Step kb: sub-steps 1..SUB-1 fetch slots 1.. of step kb+2 (PRE), the last sub-step, after the barrier,
+  // slot 0 of step kb+3 (POST).  Only steps below nk are fetched, so the last three steps are peeled:
+  // step nk-3 has no POST, step nk-2 neither, and step nk-1 also no barrier and no fragment reads.
   int c0 = 0, c1 = 1, c2 = 2;  // stages of steps kb, kb+1, kb+2
-  for (int kb = 0; kb < nk; ++kb) {
+  auto step = [&](int kb, auto PRE, auto POST, auto LAST) {
+    constexpr bool pre = decltype(PRE)::value, last = decltype(LAST)::value;
     const int k2 = (kb + 2) * BK;
     static_for<SUB - 1>([&](auto S) {
       constexpr int s = decltype(S)::value;
-      substep(ic<s & 1>{}, c0, s + 1, ic<s + 1>{}, k2, c2);
+      substep(ic<s & 1>{}, c0, s + 1, ic<s + 1>{}, k2, c2, ic<1>{}, PRE);
     });
-    // Own reads of this stage done, own DMAs of step kb+1 landed (only step
-    // kb+2's may still be in flight); the barrier makes that hold for every wave.
-    wait_counts<NDMA, 0>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    substep(ic<(SUB - 1) & 1>{}, c1, 0, ic<0>{}, (kb + 3) * BK, c0);
+    if constexpr (!last) {
+      // Own reads of this stage done, own DMAs of step kb+1 landed (with PRE only step kb+2's, NDMA of
+      // them, may still be in flight; without it none are); the barrier makes that hold for every wave.
+      if constexpr (pre)
+        wait_counts<NDMA, 0>();
+      else
+        wait_counts<0, 0>();
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    substep(ic<(SUB - 1) & 1>{}, c1, 0, ic<0>{}, (kb + 3) * BK, c0, ic<!last>{}, POST);
     const int c = c0;
     c0 = c1;
     c1 = c2;
     c2 = c;
-  }
-  // All DMAs landed and all waves past their last LDS read before the
-  // stages are reused for the output tile.
-  wait_counts<0, 0>();
+  };
+  int kb = 0;
+  for (; kb < nk - 3; ++kb) step(kb, ic<1>{}, ic<1>{}, ic<0>{});
+  if (nk >= 3) step(kb++, ic<1>{}, ic<0>{}, ic<0>{});
+  if (nk >= 2) step(kb++, ic<0>{}, ic<0>{}, ic<0>{});
+  step(kb, ic<0>{}, ic<0>{}, ic<1>{});
+  // The epilogue operands from LDS (their latency overlaps the drain), then all DMAs landed and all
+  // waves past their last LDS read before the stages are reused for the output staging.
+  float4 swv[NI][4], bfv[NI][4];
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c = wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
+      if constexpr (kI8) swv[j][g] = *reinterpret_cast<const float4*>(epi + c * 4);
+      if constexpr (HAS_BIAS) bfv[j][g] = *reinterpret_cast<const float4*>(epi + 2048 + c * 4);
+    }
+  wait_counts<0, 15>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  // Block (j, i) element (n, m): m = l32, n = 8*(r/4) + 4*half + r%4.
+  // Each wave converts its 64 x 64 sub-tile as two 32-row slabs; a slab goes to the wave's own LDS area
+  // as bf16 rows and leaves as full 128-byte row segments (8 rows per store instruction) while the next
+  // slab is converted.  Block (j, i) element (n, m): m = l32, n = 8*(r/4) + 4*half + r%4.
+  uint8_t* const wst = lds + wave * (2 * 32 * WPITCH);
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
-    const int r = wm * (BM / WM) + i * 32 + l32;
+    uint8_t* const slab = wst + i * 32 * WPITCH;
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int c = wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
-        const uint32_t bb[4] = {bv[j][g].x << 16, bv[j][g].x & 0xffff0000u, bv[j][g].y << 16,
-                                bv[j][g].y & 0xffff0000u};
+        const int cw = j * 32 + 8 * g + 4 * half;  // column within the wave's 64
         float y[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -321,39 +409,41 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
           } else {
             y[e] = __fmul_rn(acc[j][i][4 * g + e], scale);
           }
-          if (HAS_BIAS) y[e] = __fadd_rn(y[e], __uint_as_float(bb[e]));
+          if constexpr (HAS_BIAS) {
+            const float b4[4] = {bfv[j][g].x, bfv[j][g].y, bfv[j][g].z, bfv[j][g].w};
+            y[e] = __fadd_rn(y[e], b4[e]);
+          }
           if (GELU) y[e] = gelu_tanh(__uint_as_float(pack_bf16x2_hw(y[e], 0.f) << 16));
         }
-        *reinterpret_cast<uint2*>(lds + r * OUT_PITCH + c * 2) =
+        *reinterpret_cast<uint2*>(slab + l32 * WPITCH + cw * 2) =
             make_uint2(pack_bf16x2_hw(y[0], y[1]), pack_bf16x2_hw(y[2], y[3]));
-        if constexpr (kI8) {
-          if (p.acc_out) {
-            const int gm = m0 + r, gn = n0 + c;
-            if (gm < p.M && gn < p.N)
-              *reinterpret_cast<int4*>(p.acc_out + static_cast<int64_t>(gm) * p.N + gn) =
-                  make_int4(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
-          }
+        if constexpr (kI8 && ACC) {
+          const int gm = m0 + wm * (BM / WM) + i * 32 + l32, gn = n0 + wn * (BN / WN) + cw;
+          if (gm < p.M && gn < p.N)
+            *reinterpret_cast<int4*>(p.acc_out + static_cast<int64_t>(gm) * p.N + gn) =
+                make_int4(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
         }
       }
-  }
-  __syncthreads();
-  constexpr int CPR = BN * 2 / 16;  // 16-byte chunks per tile row
-  constexpr int ITERS = BM * CPR / THREADS;
-  static_assert(ITERS * THREADS == BM * CPR, "epilogue chunks");
+    // the slab's rows are read back by other lanes of this wave: LDS executes a wave's accesses in order
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int ch = lane & 7;
+    const int gn = n0 + wn * (BN / WN) + ch * 8;
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    const int id = it * THREADS + static_cast<int>(threadIdx.x);
-    const int r = id / CPR, c = id % CPR;
-    const int gm = m0 + r, gn = n0 + c * 8;
-    const uint4 v = *reinterpret_cast<const uint4*>(lds + r * OUT_PITCH + c * 16);
-    if (gm < p.M && gn < p.N) {
-      uint16_t* dst = p.y + static_cast<int64_t>(gm) * p.ldy + gn;
-      if (p.vec16 && gn + 8 <= p.N) {
-        *reinterpret_cast<uint4*>(dst) = v;
-      } else {
-        // N % 4 == 0 (checked at the entry point): the first 4 columns are in.
-        *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
-        if (gn + 8 <= p.N) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
+    for (int it = 0; it < 4; ++it) {
+      const int rr = it * 8 + (lane >> 3);
+      const uint4 v = *reinterpret_cast<const uint4*>(slab + rr * WPITCH + ch * 16);
+      const int gm = m0 + wm * (BM / WM) + i * 32 + rr;
+      if (gm < p.M && gn < p.N) {
+        uint16_t* dst = p.y + static_cast<int64_t>(gm) * p.ldy + gn;
+        if (p.vec16 && gn + 8 <= p.N) {
+          *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+          // N % 4 == 0 (checked at the entry point): the first 4 columns are in.
+          *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
+          if (gn + 8 <= p.N) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
+        }
       }
     }
   }
@@ -392,7 +482,7 @@ struct StepTarget {
 // epilogue writes straight from registers: after two lane-half swaps each
 // lane holds 8 consecutive columns of its row (16-byte stores), so the LDS
 // stages keep the next tile's data in flight.
-template <typename OP, bool HAS_BIAS, bool GELU>
+template <typename OP, bool HAS_BIAS, bool GELU, bool ACC>
 __global__ __launch_bounds__(THREADS, 1) void gemm_persistent_kernel(GemmArgs p) {
   constexpr bool kI8 = std::is_same<OP, OpI8>::value;
   constexpr int SUB = OP::SUB;
@@ -563,8 +653,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_persistent_kernel(GemmArgs p)
           }
           w[g][0] = pack_bf16x2_hw(y[0], y[1]);
           w[g][1] = pack_bf16x2_hw(y[2], y[3]);
-          if constexpr (kI8) {
-            if (p.acc_out) {
+          if constexpr (kI8 && ACC) {
+            {
               const int gn = n0 + wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
               if (gm < p.M && gn < p.N)
                 *reinterpret_cast<int4*>(p.acc_out + static_cast<int64_t>(gm) * p.N + gn) =
@@ -672,31 +762,44 @@ GemmArgs make_args(const void* a, const void* w, int64_t M, int64_t N, int64_t K
   return p;
 }
 
+template <bool PERSIST, typename OP, bool B, bool G, bool ACC>
+void launch_one(const GemmArgs& p, dim3 grid, hipStream_t stream) {
+  if constexpr (PERSIST)
+    hipLaunchKernelGGL((gemm_persistent_kernel<OP, B, G, ACC>), grid, dim3(THREADS), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, B, G, ACC>), grid, dim3(THREADS), 0, stream, p);
+}
+
+template <bool PERSIST, typename OP, bool ACC>
+void launch_kernel(const GemmArgs& p, bool bias, bool gelu, dim3 grid, hipStream_t stream) {
+  if (bias && gelu)
+    launch_one<PERSIST, OP, true, true, ACC>(p, grid, stream);
+  else if (bias)
+    launch_one<PERSIST, OP, true, false, ACC>(p, grid, stream);
+  else if (gelu)
+    launch_one<PERSIST, OP, false, true, ACC>(p, grid, stream);
+  else
+    launch_one<PERSIST, OP, false, false, ACC>(p, grid, stream);
+}
+
 template <typename OP>
 int launch(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream, const char* fn) {
   const int64_t tiles = ((static_cast<int64_t>(p.M) + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   const int cus = device_cus() / NUM_XCD * NUM_XCD;
+  const bool acc = std::is_same<OP, OpI8>::value && p.acc_out != nullptr;
   if (cus >= NUM_XCD && tiles > cus) {
-    const dim3 grid(static_cast<uint32_t>(cus)), block(THREADS);
-    if (bias && gelu)
-      hipLaunchKernelGGL((gemm_persistent_kernel<OP, true, true>), grid, block, 0, stream, p);
-    else if (bias)
-      hipLaunchKernelGGL((gemm_persistent_kernel<OP, true, false>), grid, block, 0, stream, p);
-    else if (gelu)
-      hipLaunchKernelGGL((gemm_persistent_kernel<OP, false, true>), grid, block, 0, stream, p);
+    const dim3 grid(static_cast<uint32_t>(cus));
+    if (acc)
+      launch_kernel<true, OP, true>(p, bias, gelu, grid, stream);
     else
-      hipLaunchKernelGGL((gemm_persistent_kernel<OP, false, false>), grid, block, 0, stream, p);
+      launch_kernel<true, OP, false>(p, bias, gelu, grid, stream);
     return check_launch(fn);
   }
-  const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD)), block(THREADS);
-  if (bias && gelu)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, true, true>), grid, block, 0, stream, p);
-  else if (bias)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, true, false>), grid, block, 0, stream, p);
-  else if (gelu)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, false, true>), grid, block, 0, stream, p);
+  const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD));
+  if (acc)
+    launch_kernel<false, OP, true>(p, bias, gelu, grid, stream);
   else
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, false, false>), grid, block, 0, stream, p);
+    launch_kernel<false, OP, false>(p, bias, gelu, grid, stream);
   return check_launch(fn);
 }
 
