@@ -65,8 +65,8 @@ def _gemm_case(M, N, K, seed, bias=True, gelu=False):
     (4680, 4608, 1536),   # fused QKV
     (4680, 1536, 8960),   # fc_out
     (1, 4, 16), (17, 132, 48), (300, 256, 1552), (513, 1540, 272),
-    (3000, 3204, 272),    # more tiles than CUs (persistent kernel), partial tiles, N % 8 == 4: 8-byte stores
-    (2050, 8196, 160),    # persistent, 561 tiles, K tail of 32 bytes
+    (3000, 3204, 272),    # more tiles than CUs (several rounds), partial tiles, N % 8 == 4: 8-byte stores
+    (2050, 8196, 160),    # 561 tiles, K tail of 32 bytes
 ])
 def test_gemm_exact(M, N, K):
     y, acc, oy, oacc = _gemm_case(M, N, K, seed=M + N + K)

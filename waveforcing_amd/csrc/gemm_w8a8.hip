@@ -48,9 +48,11 @@
 //    the next slab.
 //  * Tiles are ordered so that the workgroups one XCD receives (blockIdx % 8)
 //    form a contiguous range, walked in bands of 8 tile rows, so co-resident
-//    workgroups share A and W panels in that XCD's L2.
-//  * Shapes with more tiles than CUs run the persistent variant below (one
-//    workgroup per CU, tiles walked as one continuous K-step pipeline).
+//    workgroups share A and W panels in that XCD's L2.  Shapes with more
+//    tiles than CUs run several rounds of workgroups: measured against a
+//    persistent form (one workgroup per CU walking its tiles as one K-step
+//    pipeline, whose epilogue had no free LDS to stage in), the rounds are
+//    4-7 % faster on every multi-round Wan shape.
 #include <type_traits>
 #include <utility>
 
@@ -449,301 +451,6 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   }
 }
 
-// Lanes 32..63 of lo trade places with lanes 0..31 of hi (v_permlane32_swap_b32;
-// inline asm because the ROCm 7.2 builtin's second result is miscompiled, and
-// not volatile so it schedules like any other VALU instruction).
-__device__ inline void swap_halves_u32(uint32_t& lo, uint32_t& hi) {
-  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
-}
-
-struct TileMap {
-  int tiles_m, tiles_n;
-  __device__ inline void mn(int t, int& m0, int& n0) const {
-    const int per_group = GROUP_M * tiles_n;
-    const int first_m = (t / per_group) * GROUP_M;
-    const int band = min(tiles_m - first_m, GROUP_M);
-    m0 = (first_m + (t % per_group) % band) * BM;
-    n0 = ((t % per_group) / band) * BN;
-  }
-};
-
-struct StepTarget {
-  int a_base, w_base, k0;
-  bool valid;
-};
-
-// Persistent variant for shapes with more tiles than CUs: one workgroup per
-// CU walks its tiles (the XCD's contiguous tile range, strided by the
-// workgroups of the XCD) as one flat sequence of K steps, so the DMA ring
-// runs on across tile boundaries and only the first tile's loads are
-// exposed.  Its DMA targets advance one step at a time (the tile mapping
-// is evaluated only when a target crosses into the next tile).  The
-// epilogue operands are loaded during a tile's last K step, and the
-// epilogue writes straight from registers: after two lane-half swaps each
-// lane holds 8 consecutive columns of its row (16-byte stores), so the LDS
-// stages keep the next tile's data in flight.
-template <typename OP, bool HAS_BIAS, bool GELU, bool ACC>
-__global__ __launch_bounds__(THREADS, 1) void gemm_persistent_kernel(GemmArgs p) {
-  constexpr bool kI8 = std::is_same<OP, OpI8>::value;
-  constexpr int SUB = OP::SUB;
-  constexpr int PIECES = OP::PIECES;
-  constexpr int CPS = BK / 16 / SUB;
-  static_assert(CPS == 2 * PIECES, "sub-step geometry");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[ST * STAGE];
-
-  TileMap tm;
-  tm.tiles_m = (p.M + BM - 1) / BM;
-  tm.tiles_n = (p.N + BN - 1) / BN;
-  const int n_tiles = tm.tiles_m * tm.tiles_n;
-  const int per_wg = gridDim.x / NUM_XCD;  // workgroups per XCD (grid is a multiple of 8)
-  const int xcd = blockIdx.x % NUM_XCD;
-  const int slot = blockIdx.x / NUM_XCD;
-  const int per_xcd = (n_tiles + NUM_XCD - 1) / NUM_XCD;
-  const int t_first = xcd * per_xcd + slot;
-  const int t_end = min((xcd + 1) * per_xcd, n_tiles);
-  if (t_first >= t_end) return;
-  const int my_tiles = (t_end - t_first + per_wg - 1) / per_wg;
-  const int nk = (p.K + BK - 1) / BK;
-  const int S = my_tiles * nk;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN;
-  const int wn = wave % WN;
-  const int l32 = lane & 31;
-  const int half = lane >> 5;
-
-  const __amdgpu_buffer_rsrc_t rsrc_a =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), 0, p.M * p.K, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rsrc_w =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.w), 0, p.N * p.K, kBufferRsrcWord3);
-
-  int loff[NDMA], dcol[NDMA];
-#pragma unroll
-  for (int j = 0; j < NDMA; ++j) {
-    const bool is_a = j < NBA;
-    const int r = ((is_a ? j : j - NBA) * NW + wave) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ ((r >> 1) & 7);
-    dcol[j] = c * 16;
-    loff[j] = r * p.K + c * 16;
-  }
-  // DMA targets advance one step at a time; the tile mapping is evaluated only at tile boundaries
-  const int k_end = nk * BK;
-  auto first_target = [&](int lt) {
-    StepTarget t;
-    t.valid = lt < my_tiles;
-    t.k0 = 0;
-    int m0 = 0, n0 = 0;
-    tm.mn(t_first + lt * per_wg, m0, n0);
-    t.a_base = m0 * p.K;
-    t.w_base = n0 * p.K;
-    return t;
-  };
-  int t_lt = 0;   // local tile of the most advanced target
-  auto advance = [&](StepTarget t) {
-    t.k0 += BK;
-    t.a_base += BK;
-    t.w_base += BK;
-    if (t.k0 >= k_end) {
-      ++t_lt;
-      t = first_target(t_lt);
-    }
-    return t;
-  };
-  auto dma = [&](auto J, const StepTarget& t, int stage) {
-    constexpr int j = decltype(J)::value;
-    const int off = (t.valid && t.k0 + dcol[j] < p.K) ? loff[j] + (j < NBA ? t.a_base : t.w_base) : kOutOfRange;
-    if constexpr (j < NBA)
-      dma16(rsrc_a, lds + stage * STAGE + (j * NW + wave) * 1024, off);
-    else
-      dma16(rsrc_w, lds + stage * STAGE + A_BYTES + ((j - NBA) * NW + wave) * 1024, off);
-  };
-
-  const int x = (l32 >> 1) & 7;
-  const int lane_a = (wm * (BM / WM) + l32) * BK;
-  const int lane_b = A_BYTES + (wn * (BN / WN) + l32) * BK;
-  int koff[SUB][PIECES];
-#pragma unroll
-  for (int s = 0; s < SUB; ++s)
-#pragma unroll
-    for (int e = 0; e < PIECES; ++e) koff[s][e] = 16 * ((s * CPS + half * PIECES + e) ^ x);
-
-  typename OP::acc_t acc[NI][MI];
-#pragma unroll
-  for (int j = 0; j < NI; ++j)
-#pragma unroll
-    for (int i = 0; i < MI; ++i) acc[j][i] = typename OP::acc_t{};
-  v4i fa[2][MI][PIECES], fw[2][NI][PIECES];
-
-  auto frag_read = [&](auto O, auto B, int stage, int s) {
-    constexpr int o = decltype(O)::value;
-    constexpr int b = decltype(B)::value;
-    constexpr int q = o / PIECES, e = o % PIECES;
-    if constexpr (q < MI)
-      fa[b][q][e] = *reinterpret_cast<const v4i*>(lds + stage * STAGE + lane_a + koff[s][e] + q * 32 * BK);
-    else
-      fw[b][q - MI][e] = *reinterpret_cast<const v4i*>(lds + stage * STAGE + lane_b + koff[s][e] + (q - MI) * 32 * BK);
-  };
-  auto substep = [&](auto B, int rstage, int rs, auto SLOT, const StepTarget& dt, int dstage) {
-    constexpr int b = decltype(B)::value;
-    constexpr int slot_ = decltype(SLOT)::value;
-    constexpr int d_lo = (slot_ * NDMA + SUB - 1) / SUB;
-    constexpr int d_hi = ((slot_ + 1) * NDMA + SUB - 1) / SUB;
-    constexpr int NMF = MI * NI, NRD = (MI + NI) * PIECES;
-    constexpr int NOPS = NRD + d_hi - d_lo;
-    static_for<NMF>([&](auto Q) {
-      constexpr int q = decltype(Q)::value;
-      constexpr int jj = q / MI, ii = q % MI;
-      acc[jj][ii] = OP::mfma(fw[b][jj], fa[b][ii], acc[jj][ii]);
-      constexpr int o_lo = (q * NOPS + NMF - 1) / NMF, o_hi = ((q + 1) * NOPS + NMF - 1) / NMF;
-      static_for<o_hi - o_lo>([&](auto U) {
-        constexpr int o = o_lo + decltype(U)::value;
-        if constexpr (o < NRD)
-          frag_read(ic<o>{}, ic<b ^ 1>{}, rstage, rs);
-        else
-          dma(ic<d_lo + o - NRD>{}, dt, dstage);
-      });
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  };
-
-  // epilogue operands of the compute tile
-  float sxv[MI];
-  float4 swv[NI][4];
-  uint2 bv[NI][4];
-  float scale = 0.f;
-  auto load_epilogue = [&](int m0, int n0) {
-    if constexpr (kI8) {
-#pragma unroll
-      for (int i = 0; i < MI; ++i) sxv[i] = p.sx[min(m0 + wm * (BM / WM) + i * 32 + l32, p.M - 1)];
-    } else {
-      scale = p.sx[0] * p.sw[0];
-    }
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int gn = min(n0 + wn * (BN / WN) + j * 32 + 8 * g + 4 * half, p.N - 4);
-        if constexpr (kI8) swv[j][g] = *reinterpret_cast<const float4*>(p.sw + gn);
-        bv[j][g] = HAS_BIAS ? *reinterpret_cast<const uint2*>(p.bias + gn) : make_uint2(0, 0);
-      }
-  };
-  auto epilogue = [&](int m0, int n0) {
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int gm = m0 + wm * (BM / WM) + i * 32 + l32;
-#pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        uint32_t w[4][2];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const uint32_t bb[4] = {bv[j][g].x << 16, bv[j][g].x & 0xffff0000u, bv[j][g].y << 16,
-                                  bv[j][g].y & 0xffff0000u};
-          float y[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if constexpr (kI8) {
-              const float sw4[4] = {swv[j][g].x, swv[j][g].y, swv[j][g].z, swv[j][g].w};
-              y[e] = __fmul_rn(__fmul_rn(static_cast<float>(acc[j][i][4 * g + e]), sxv[i]), sw4[e]);
-            } else {
-              y[e] = __fmul_rn(acc[j][i][4 * g + e], scale);
-            }
-            if (HAS_BIAS) y[e] = __fadd_rn(y[e], __uint_as_float(bb[e]));
-            if (GELU) y[e] = gelu_tanh(__uint_as_float(pack_bf16x2_hw(y[e], 0.f) << 16));
-          }
-          w[g][0] = pack_bf16x2_hw(y[0], y[1]);
-          w[g][1] = pack_bf16x2_hw(y[2], y[3]);
-          if constexpr (kI8 && ACC) {
-            {
-              const int gn = n0 + wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
-              if (gm < p.M && gn < p.N)
-                *reinterpret_cast<int4*>(p.acc_out + static_cast<int64_t>(gm) * p.N + gn) =
-                    make_int4(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
-            }
-          }
-        }
-        // lanes l < 32 hold columns 8g + 0..3, lanes l + 32 columns 8g + 4..7 of row gm; after the swaps
-        // lane l holds columns 0..7 and 16..23, lane l + 32 columns 8..15 and 24..31 of the 32-column block
-        swap_halves_u32(w[0][0], w[1][0]);
-        swap_halves_u32(w[0][1], w[1][1]);
-        swap_halves_u32(w[2][0], w[3][0]);
-        swap_halves_u32(w[2][1], w[3][1]);
-        if (gm < p.M) {
-          const int gn = n0 + wn * (BN / WN) + j * 32 + 8 * half;
-          uint16_t* row = p.y + static_cast<int64_t>(gm) * p.ldy;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int c = gn + 16 * h;
-            const uint4 v = make_uint4(w[2 * h][0], w[2 * h][1], w[2 * h + 1][0], w[2 * h + 1][1]);
-            if (p.vec16 && c + 8 <= p.N) {
-              *reinterpret_cast<uint4*>(row + c) = v;
-            } else if (c < p.N) {
-              *reinterpret_cast<uint2*>(row + c) = make_uint2(v.x, v.y);
-              if (c + 8 <= p.N) *reinterpret_cast<uint2*>(row + c + 4) = make_uint2(v.z, v.w);
-            }
-          }
-        }
-      }
-    }
-  };
-
-  // prologue: steps 0 and 1 whole, slot 0 of step 2, fragments of step 0's first sub-step
-  StepTarget ta, tb;   // targets of steps s + 2 and s + 3
-  {
-    const StepTarget t0 = first_target(0);
-    const StepTarget t1 = advance(t0);
-    const StepTarget t2 = advance(t1);
-    ta = t2;
-    tb = advance(t2);
-    static_for<NDMA>([&](auto J) { dma(J, t0, 0); });
-    static_for<NDMA>([&](auto J) { dma(J, t1, 1); });
-    wait_counts<NDMA, 0>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    static_for<(NDMA + SUB - 1) / SUB>([&](auto J) { dma(J, t2, 2); });
-    static_for<(MI + NI) * PIECES>([&](auto O) { frag_read(O, ic<0>{}, 0, 0); });
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  int c0 = 0, c1 = 1, c2 = 2;
-  int kb = 0, lt = 0;
-  int cm0, cn0;
-  tm.mn(t_first, cm0, cn0);
-  for (int s = 0; s < S; ++s) {
-    const bool last = kb == nk - 1;
-    if (last) load_epilogue(cm0, cn0);
-    static_for<SUB - 1>([&](auto Sx) {
-      constexpr int ss = decltype(Sx)::value;
-      substep(ic<ss & 1>{}, c0, ss + 1, ic<ss + 1>{}, ta, c2);
-    });
-    wait_counts<NDMA, 0>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    substep(ic<(SUB - 1) & 1>{}, c1, 0, ic<0>{}, tb, c0);
-    const int c = c0;
-    c0 = c1;
-    c1 = c2;
-    c2 = c;
-    ta = tb;
-    tb = advance(tb);
-    if (last) {
-      epilogue(cm0, cn0);
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int i = 0; i < MI; ++i) acc[j][i] = typename OP::acc_t{};
-      kb = 0;
-      ++lt;
-      if (lt < my_tiles) tm.mn(t_first + lt * per_wg, cm0, cn0);
-    } else {
-      ++kb;
-    }
-  }
-  // the DMAs into stages past the last step must land before the workgroup's LDS is released
-  wait_counts<0, 15>();
-}
-
 GemmArgs make_args(const void* a, const void* w, int64_t M, int64_t N, int64_t K, const float* sx, const float* sw,
                    const void* bias, void* y, int64_t ldy, int32_t* acc_out) {
   GemmArgs p;
@@ -762,44 +469,27 @@ GemmArgs make_args(const void* a, const void* w, int64_t M, int64_t N, int64_t K
   return p;
 }
 
-template <bool PERSIST, typename OP, bool B, bool G, bool ACC>
-void launch_one(const GemmArgs& p, dim3 grid, hipStream_t stream) {
-  if constexpr (PERSIST)
-    hipLaunchKernelGGL((gemm_persistent_kernel<OP, B, G, ACC>), grid, dim3(THREADS), 0, stream, p);
-  else
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, B, G, ACC>), grid, dim3(THREADS), 0, stream, p);
-}
-
-template <bool PERSIST, typename OP, bool ACC>
+template <typename OP, bool ACC>
 void launch_kernel(const GemmArgs& p, bool bias, bool gelu, dim3 grid, hipStream_t stream) {
+  const dim3 block(THREADS);
   if (bias && gelu)
-    launch_one<PERSIST, OP, true, true, ACC>(p, grid, stream);
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, true, true, ACC>), grid, block, 0, stream, p);
   else if (bias)
-    launch_one<PERSIST, OP, true, false, ACC>(p, grid, stream);
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, true, false, ACC>), grid, block, 0, stream, p);
   else if (gelu)
-    launch_one<PERSIST, OP, false, true, ACC>(p, grid, stream);
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, false, true, ACC>), grid, block, 0, stream, p);
   else
-    launch_one<PERSIST, OP, false, false, ACC>(p, grid, stream);
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, false, false, ACC>), grid, block, 0, stream, p);
 }
 
 template <typename OP>
 int launch(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream, const char* fn) {
   const int64_t tiles = ((static_cast<int64_t>(p.M) + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  const int cus = device_cus() / NUM_XCD * NUM_XCD;
-  const bool acc = std::is_same<OP, OpI8>::value && p.acc_out != nullptr;
-  if (cus >= NUM_XCD && tiles > cus) {
-    const dim3 grid(static_cast<uint32_t>(cus));
-    if (acc)
-      launch_kernel<true, OP, true>(p, bias, gelu, grid, stream);
-    else
-      launch_kernel<true, OP, false>(p, bias, gelu, grid, stream);
-    return check_launch(fn);
-  }
   const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD));
-  if (acc)
-    launch_kernel<false, OP, true>(p, bias, gelu, grid, stream);
+  if (std::is_same<OP, OpI8>::value && p.acc_out != nullptr)
+    launch_kernel<OP, true>(p, bias, gelu, grid, stream);
   else
-    launch_kernel<false, OP, false>(p, bias, gelu, grid, stream);
+    launch_kernel<OP, false>(p, bias, gelu, grid, stream);
   return check_launch(fn);
 }
 
