@@ -20,18 +20,6 @@ int set_error(int status, const char* fmt, ...) {
   return status;
 }
 
-int device_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(static_cast<int>(e), "%s: launch failed: %s", what, hipGetErrorString(e));

@@ -28,10 +28,6 @@ int check_launch(const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Compute units of the current device (looked up once per device; 0 if the
-// query fails, which sends callers to their non-persistent launch).
-int device_cus();
-
 // ------------------------------------------------------------------- bf16
 // bf16 -> fp32 is exact: the bf16 bits are the high half of the fp32 bits.
 __device__ __host__ inline float bf16_lo_to_f32(uint32_t packed) {
