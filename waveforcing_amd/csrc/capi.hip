@@ -1,5 +1,4 @@
 // Status reporting of the C ABI and the elementwise FP8 cast entry points.
-#include <atomic>
 #include <cstring>
 
 #include "fp8_codec.hpp"
