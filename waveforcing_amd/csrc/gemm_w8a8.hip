@@ -375,20 +375,27 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   if (nk >= 3) step(kb++, ic<1>{}, ic<0>{}, ic<0>{});
   if (nk >= 2) step(kb++, ic<0>{}, ic<0>{}, ic<0>{});
   step(kb, ic<0>{}, ic<0>{}, ic<1>{});
-  // The epilogue operands from LDS (their latency overlaps the drain), then all DMAs landed and all
-  // waves past their last LDS read before the stages are reused for the output staging.
+  // The epilogue operands from LDS, then all DMAs landed, all LDS accesses done and all waves past
+  // their last LDS read before the stages are reused for the output staging.  The fp32 bias is wave 1's
+  // write after the prologue barrier: with two or more K steps the first step's barrier (after an LDS
+  // wait) has published it, so the operands are read before the drain to overlap it; with one K step
+  // only the barrier below publishes it.
   float4 swv[NI][4], bfv[NI][4];
+  auto read_epi = [&]() {
 #pragma unroll
-  for (int j = 0; j < NI; ++j)
+    for (int j = 0; j < NI; ++j)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int c = wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
-      if constexpr (kI8) swv[j][g] = *reinterpret_cast<const float4*>(epi + c * 4);
-      if constexpr (HAS_BIAS) bfv[j][g] = *reinterpret_cast<const float4*>(epi + 2048 + c * 4);
-    }
-  wait_counts<0, 15>();
+      for (int g = 0; g < 4; ++g) {
+        const int c = wn * (BN / WN) + j * 32 + 8 * g + 4 * half;
+        if constexpr (kI8) swv[j][g] = *reinterpret_cast<const float4*>(epi + c * 4);
+        if constexpr (HAS_BIAS) bfv[j][g] = *reinterpret_cast<const float4*>(epi + 2048 + c * 4);
+      }
+  };
+  if (nk >= 2) read_epi();
+  wait_counts<0, 0>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  if (nk < 2) read_epi();
 
   // Each wave converts its 64 x 64 sub-tile as two 32-row slabs; a slab goes to the wave's own LDS area
   // as bf16 rows and leaves as full 128-byte row segments (8 rows per store instruction) while the next
