@@ -414,6 +414,33 @@ def bench_dit(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
     return out
 
 
+def bench_generate(steps: int, warmup: int, dev: str, chunks: int = 12):
+    """WavefrontDenoiser.generate: one stream of `chunks` 3-frame chunks from noise [1, 16, 3 chunks, 60, 104] to
+    clean latents through the 30-block 1.3B DiT (rf_step 4, the four warped DMD steps, 21-frame window, 512-token
+    text context): chunks + 4 ticks, each the store pass and the active denoise ranks as a layer wavefront, the
+    re-noising between steps included; the exchange is reset at the start of each stream.  The ramp-up and drain
+    ticks hold fewer passes than the steady state."""
+    from waveforcing_amd.dit import QuantizedWanDiT, random_dit_params
+    from waveforcing_amd.stack import QuantizedWanStack
+    from waveforcing_amd.wavefront import WavefrontDenoiser
+
+    frames, H, W = 3, 60, 104
+    st = QuantizedWanStack.random("1.3b", seed=100, device=dev, tokens_per_frame=(H // 2) * (W // 2),
+                                  frames_per_chunk=frames, max_attn_frames=21, rf_step=4)
+    dit = QuantizedWanDiT(random_dit_params(st.blocks[0].dim, seed=7, device=dev), st)
+    g = torch.Generator(device=dev).manual_seed(6)
+    dit.set_text(torch.randn((512, 4096), generator=g, device=dev).to(torch.bfloat16))
+    noise = torch.randn((1, 16, frames * chunks, H, W), generator=g, device=dev).to(torch.bfloat16)
+    den = WavefrontDenoiser(dit)
+    ms = _timed(lambda: den.generate(noise, concurrent=True), steps, warmup)
+    ticks = chunks + den.rf_step
+    out = {"ms_per_stream": ms, "chunks": chunks, "ticks": ticks, "ms_per_tick_mean": ms / ticks,
+           "latent_frames_per_s": frames * chunks / (ms * 1e-3), "latent": [1, 16, frames * chunks, H, W]}
+    del den, dit, st
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_copy(steps: int, warmup: int, dev: str):
     """A plain device copy of 1 GiB (read 1 GiB + write 1 GiB): calibrates the HBM byte counters."""
     src = torch.empty((1 << 30,), dtype=torch.uint8, device=dev).fill_(1)
@@ -575,7 +602,7 @@ def main() -> None:
                     help="minimum untimed warm-up of the KV workloads (profiler runs use 0)")
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
-                                       "tick_1p3b", "copy"],
+                                       "tick_1p3b", "generate_1p3b", "copy"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -595,6 +622,7 @@ def main() -> None:
               "block_14b": lambda s, w, d: bench_block("14b", s, w, d), "exchange_1p3b": bench_exchange,
               "stack_1p3b": bench_stack, "stack_14b": lambda s, w, d: bench_stack(s, w, d, "14b"),
               "dit_1p3b": bench_dit, "tick_1p3b": lambda s, w, d: bench_stack(s, w, d, ticks_only=True),
+              "generate_1p3b": bench_generate,
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
@@ -609,6 +637,7 @@ def main() -> None:
     stk = bench_stack(max(3, args.steps // 10), 1, dev)
     stk14 = bench_stack(3, 1, dev, "14b")
     dit = bench_dit(max(3, args.steps // 10), 1, dev)
+    gen = bench_generate(1, 1, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     cpu_extra = None if args.no_cpu_baseline else cpu_baseline_extra()
     # one launch per step: the launch duration is the step time
@@ -701,6 +730,13 @@ def main() -> None:
             "dit_forward_note": "the whole Wan-1.3B DiT forward of one chunk, noisy latent [1,16,3,60,104] -> x0 "
                                 "(patch embedding, time embedding, 30 blocks, head, unpatchify, flow -> x0) as rank "
                                 "0's pass of the same steady-state tick (37440-key context), timestep 1000",
+            "generate_1p3b_ms_per_stream": round(gen["ms_per_stream"], 1),
+            "generate_1p3b_ms_per_tick_mean": round(gen["ms_per_tick_mean"], 2),
+            "generate_1p3b_latent_frames_per_s": round(gen["latent_frames_per_s"], 2),
+            "generate_note": f"WavefrontDenoiser.generate of a {gen['chunks']}-chunk stream (latent "
+                             f"{gen['latent']}) from noise to clean latents: {gen['ticks']} ticks of the store pass "
+                             "and the active denoise ranks as a layer wavefront through the 30-block 1.3B DiT, "
+                             "re-noising between DMD steps included; ramp-up and drain ticks hold fewer passes",
             "dit_block_1p3b_ms_per_chunk": round(b13["ms"], 4),
             "dit_block_14b_ms_per_chunk": round(b14["ms"], 4),
             "dit_block_note": "one block, 4680-token 3-frame chunk, 37440-key FP8 paged self-attn context, "

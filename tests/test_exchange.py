@@ -182,3 +182,34 @@ def test_capacity_guard_refuses_pools_above_ninety_percent_of_free(monkeypatch):
         ex.check_capacity(901, "cuda:0")
     with pytest.raises(RuntimeError, match="90% of free"):
         ex.PagedExchange(n_layers=30, n_heads=12, tokens_per_frame=1560, device="cuda:0")
+
+
+def test_reset_starts_a_new_stream_with_the_same_contexts():
+    """After reset (the fresh clean lists of each run of the tick loop, engine.py:294) a second stream sees
+    the same slot contexts as the first; a reset inside a tick is refused."""
+    npb, L, rf_step, num_chunks = 3, 2, 4, 10
+    x = ex.PagedExchange(n_layers=L, n_heads=1, tokens_per_frame=16, frames_per_chunk=npb, max_attn_frames=21,
+                         rf_step=rf_step, device="cpu")
+
+    def stream():
+        seen = []
+        for t in range(num_chunks + rf_step):
+            plan = x.begin_tick_at(t, num_chunks)
+            passes = ([x.store_pass()] if plan.store_active else []) + \
+                     [x.denoise_pass(r) for r in sorted(plan.act_ranks, reverse=True)]
+            for p in passes:
+                for layer in range(L):
+                    slots, own = x.context_slots(layer, p)
+                    seen.append((t, p.kind, p.chunk, layer, tuple(slots), own))
+            x.end_tick()
+        return seen
+
+    first = stream()
+    assert len(x.clean[0]) == 8
+    x.begin_tick_at(0, num_chunks)
+    with pytest.raises(RuntimeError, match="tick is in progress"):
+        x.reset()
+    x.abort_tick()
+    x.reset()
+    assert all(not c for c in x.clean) and all(len(f) == x.n_slots for f in x._free)
+    assert stream() == first

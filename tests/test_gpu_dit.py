@@ -163,7 +163,8 @@ def test_dit_concurrent_tick_is_bit_identical():
 
 def test_wavefront_generate_sequential_and_concurrent_agree():
     """WavefrontDenoiser.generate over 5 chunks at rf_step 4 (the loop of engine.py:289-560 on one GPU):
-    the sequential and the concurrent tick give the same clean latents, bit for bit; chunk 0 -- which has
+    the sequential and the concurrent tick give the same clean latents, bit for bit, and so does a second
+    stream on the same DiT (the exchange reset between streams); chunk 0 -- which has
     no older chunk to attend to -- equals its trajectory replayed alone on a fresh DiT (rank 0's pass at each
     DMD step through forward_chunk, re-noised between steps with seed 1000 * 0 + stage)."""
     from waveforcing_amd.schedule import det_renoise
@@ -192,6 +193,10 @@ def test_wavefront_generate_sequential_and_concurrent_agree():
     assert torch.equal(seq, con)
     # every chunk's store pass added one clean page per layer
     assert all(len(c) == n_chunks for c in seq_dit.stack.exchange.clean)
+    # a second stream on the same DiT starts from emptied clean lists and repeats the first exactly
+    again = WavefrontDenoiser(seq_dit).generate(noise, concurrent=True)
+    torch.cuda.synchronize()
+    assert torch.equal(again, seq)
 
     alone = make()
     dsl = alone.schedule.warp()

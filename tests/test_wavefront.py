@@ -6,7 +6,7 @@ the re-noising replaced by cheap stand-ins so every hand-off can be followed.
   context noise, which is the chunk's output; the stand-in x0 depends on the timestep and the stand-in
   re-noising on (timestep, chunk, stage), so a wrong step, chunk or seed changes the result;
 * every tick's plan, ranks and chunks follow the reference's schedule (checked inside the stand-in tick);
-* a stream cannot start on an exchange that already holds clean chunks.
+* every stream starts on emptied clean lists (the exchange is reset), and bad noise shapes are refused.
 """
 
 import types
@@ -33,7 +33,14 @@ def _renoise(x0_bcthw, next_t, chunk, stage, schedule, out=None):
 class _FakeDiT:
     def __init__(self, rf_step):
         self.schedule = FlowMatchSchedule()
-        self.stack = types.SimpleNamespace(exchange=types.SimpleNamespace(rf_step=rf_step, npb=NPB, clean=[[], []]))
+        ex = types.SimpleNamespace(rf_step=rf_step, npb=NPB, clean=[[], []], resets=0)
+
+        def reset():
+            ex.resets += 1
+            ex.clean = [[], []]
+
+        ex.reset = reset
+        self.stack = types.SimpleNamespace(exchange=ex)
         self.seen = []
 
     def tick(self, plan, inputs, concurrent=False):
@@ -78,13 +85,17 @@ def test_generate_follows_each_chunks_trajectory(monkeypatch, rf_step, steps):
     assert dit.seen == want
 
 
-def test_generate_refuses_a_used_exchange_and_bad_shapes():
+def test_generate_resets_the_exchange_and_refuses_bad_shapes(monkeypatch):
+    monkeypatch.setattr(wf, "det_renoise", _renoise)
     dit = _FakeDiT(2)
     den = wf.WavefrontDenoiser(dit, steps=(1000, 500))
     with pytest.raises(ValueError, match="split into chunks"):
         den.generate(torch.zeros((1, 16, 4, H, W), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="bf16"):
+        den.generate(torch.zeros((1, 16, 3, H, W), dtype=torch.float32))
+    assert dit.stack.exchange.resets == 0
     dit.stack.exchange.clean = [[object()], [object()]]
-    with pytest.raises(RuntimeError, match="clean chunks"):
-        den.generate(torch.zeros((1, 16, 3, H, W), dtype=torch.bfloat16))
+    den.generate(torch.zeros((1, 16, 3, H, W), dtype=torch.bfloat16))
+    assert dit.stack.exchange.resets == 1
     with pytest.raises(ValueError, match="rf_step"):
         wf.WavefrontDenoiser(dit, steps=(1000, 750, 500))

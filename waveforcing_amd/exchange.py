@@ -366,6 +366,23 @@ class PagedExchange:
         self._store = None
         self._plan = None
 
+    def reset(self) -> None:
+        """Start a new stream: empty every layer's clean list and return every slot, as each run of the
+        reference's tick loop starts from fresh clean lists (engine.py:294).  The anchor K buffer is kept
+        for reuse."""
+        if self._plan is not None:
+            raise RuntimeError("[paged] a tick is in progress (end_tick / abort_tick first)")
+        for L in range(self.n_layers):
+            self.clean[L] = []
+            self._free[L] = list(range(self.n_slots))
+            self._inflight[L] = {}
+        self._live = {}
+        self._store = None
+        self._anchor_rot = None
+        self._clean_version += 1
+        self._prepared = None
+        self._geometry = None
+
     def abort_tick(self) -> None:
         """Return every slot the tick holds without promoting anything."""
         for L, slot in self._live.items():

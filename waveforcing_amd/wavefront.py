@@ -47,15 +47,14 @@ class WavefrontDenoiser:
         """Denoise ``noise`` [1, 16, F, H, W] bf16 (F a multiple of the chunk's frames) chunk by chunk through
         the wavefront; returns the clean latents [1, 16, F, H, W] (each chunk's store-pass input).
         ``on_chunk(c, latent)``, if given, is called as each chunk completes (the reference's output queue,
-        engine.py:391-403).  The exchange must be fresh (no clean chunks): the stream starts at chunk 0."""
+        engine.py:391-403).  The stream starts at chunk 0 on emptied clean lists (PagedExchange.reset,
+        engine.py:294)."""
         if noise.dim() != 5 or noise.shape[0] != 1 or noise.shape[1] != IN_DIM or noise.dtype != torch.bfloat16:
             raise ValueError(f"noise must be bf16 [1, {IN_DIM}, F, H, W], got {tuple(noise.shape)} {noise.dtype}")
         npb, rf = self.npb, self.rf_step
         if noise.shape[2] % npb:
             raise ValueError(f"{noise.shape[2]} latent frames do not split into chunks of {npb}")
-        ex = self.dit.stack.exchange
-        if any(ex.clean):
-            raise RuntimeError("the exchange already holds clean chunks; generate() starts a stream at chunk 0")
+        self.dit.stack.exchange.reset()
         num_chunks = noise.shape[2] // npb
         out = torch.empty_like(noise)
         handoff: dict = {}       # rank (or "store") -> latent [1, 16, npb, H, W] it takes at the next tick
