@@ -206,3 +206,41 @@ def test_wavefront_generate_sequential_and_concurrent_agree():
         lat = det_renoise(x0, dsl[r + 1], 0, r, alone.schedule) if r < 3 else x0
     torch.cuda.synchronize()
     assert torch.equal(seq[:, :, 0:3], lat)
+
+
+def test_store_pass_stops_after_the_last_layers_kv():
+    """A store pass whose output is dropped (run_pass with want_x0=False) runs its last layer only up to the
+    K/V pack: over three stored chunks the pool's codes and scales and the anchor's un-rotated K equal those
+    the whole pass (through the last layer's FFN and the head) leaves, bit for bit, and so does the x0 of a
+    denoise pass over that context."""
+    from waveforcing_amd.exchange import TickPlan
+
+    dim, heads, ffn, layers, H, W = 256, 2, 512, 2, 16, 16
+    bparams, dparams, noisy, ctx = _dit_case(dim, heads, ffn, layers, H, W, seed=51)
+    page = (H // 2) * (W // 2)
+
+    def make():
+        blocks = [QuantizedWanBlock(p, heads, DEV) for p in bparams]
+        dit = QuantizedWanDiT(dparams, QuantizedWanStack(blocks, PagedExchange(layers, heads, page, 3, 21, rf_step=4,
+                                                                                device=DEV)))
+        dit.set_text(ctx.to(DEV))
+        return dit
+
+    short, full = make(), make()
+    g = torch.Generator().manual_seed(52)
+    for c in range(3):
+        lat = torch.randn((1, 16, 3, H, W), generator=g).to(BF16).to(DEV)
+        short.forward_chunk(lat, 0.0, c, store=True)
+        ex = full.stack.exchange
+        ex.begin_tick(TickPlan(c + 4, [], True, 0, 0))
+        full.run_pass(lat, 0.0, ex.store_pass(), want_x0=True)
+        ex.end_tick()
+    torch.cuda.synchronize()
+    a, b = short.stack.exchange, full.stack.exchange
+    for name in ("k_codes", "v_codes", "k_scales", "v_scales"):
+        assert torch.equal(getattr(a.pool, name), getattr(b.pool, name)), name
+    assert torch.equal(a.anchor_ku, b.anchor_ku)
+    x0a = short.forward_chunk(noisy.to(DEV), 937.5, chunk=3)
+    x0b = full.forward_chunk(noisy.to(DEV), 937.5, chunk=3)
+    torch.cuda.synchronize()
+    assert torch.equal(x0a, x0b)

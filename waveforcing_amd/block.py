@@ -261,7 +261,7 @@ class QuantizedWanBlock:
     def forward(self, x: torch.Tensor, e: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pool: Fp8PagePool,
                 context_table: PageTable, own_table: PageTable, n_context: int, text_kv,
                 unroped_k_out: torch.Tensor | None = None, es: torch.Tensor | None = None, pending=None,
-                defer_residual: bool = False, ws: dict | None = None):
+                defer_residual: bool = False, ws: dict | None = None, kv_only: bool = False):
         """Advance x [T, dim] bf16 in place through the block.
 
         e: [F, 6, dim] bf16 time modulation of the chunk's F frames.
@@ -284,6 +284,10 @@ class QuantizedWanBlock:
         ws: optional activation buffers from :meth:`new_workspace` (passes that run
         concurrently on different streams each bring their own); default: the
         block's own, shared with the blocks of its stack.
+        kv_only: stop once this chunk's K and V are in its pages (and the
+        un-rotated K in ``unroped_k_out``), for a pass whose output nobody reads;
+        x then holds the block's input with ``pending`` applied, and (x, None)
+        is returned.
         """
         T, dim = x.shape
         F = e.shape[0]
@@ -314,6 +318,9 @@ class QuantizedWanBlock:
         q, k, v = qkv[:, :dim], qkv[:, dim:2 * dim], qkv[:, 2 * dim:]
         # q and K: RMSNorm + RoPE in one pass (q in place: each row is read whole before it is
         # written), K FP8-packed into this chunk's pages and V packed beside it
+        if kv_only:
+            pool.pack_k_norm_rope(k, v, own_table, self.norm_k, EPS, (cos, sin), ku_out=unroped_k_out)
+            return x, None
         pool.pack_k_norm_rope(k, v, own_table, self.norm_k, EPS, (cos, sin), ku_out=unroped_k_out, q=q,
                               norm_q=self.norm_q)
         ctx = PagedKV(pool, context_table, n_context)

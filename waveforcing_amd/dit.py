@@ -234,9 +234,11 @@ class QuantizedWanDiT:
         ws = self._workspace(Fr * hp * wp)
         x = self._embed(noisy, ws)
         e, e0 = self.time_modulation(t, Fr)
-        self.stack.run_pass(x, e0, p, hp, wp)
         if not want_x0:
+            # only the pages matter: the last layer stops after publishing its K/V
+            self.stack.run_pass(x, e0, p, hp, wp, kv_only_last=True)
             return None
+        self.stack.run_pass(x, e0, p, hp, wp)
         return self._head(x, e, noisy, t, ws, self._x0_buffer(noisy, x0_out))
 
     def tick(self, plan: TickPlan, inputs: dict, concurrent: bool = False) -> dict:

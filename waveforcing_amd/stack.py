@@ -69,21 +69,30 @@ class QuantizedWanStack:
         """Cross-attention K/V of the text context for every layer (once per request)."""
         self.text_kv = [blk.text_kv(context) for blk in self.blocks]
 
-    def run_pass(self, x: torch.Tensor, e: torch.Tensor, p: Pass, height: int, width: int) -> torch.Tensor:
-        """Advance x [T, dim] bf16 in place through every layer as pass ``p`` of the current tick."""
+    def run_pass(self, x: torch.Tensor, e: torch.Tensor, p: Pass, height: int, width: int,
+                 kv_only_last: bool = False) -> torch.Tensor | None:
+        """Advance x [T, dim] bf16 in place through every layer as pass ``p`` of the current tick.  With
+        ``kv_only_last`` (a store pass whose output is dropped) the last layer stops once its K/V are
+        published: every page the pass writes is the same, x is left mid-layer and None is returned."""
         if self.text_kv is None:
             raise RuntimeError("set_text() first")
+        if kv_only_last and p.kind != "store":
+            raise ValueError("only a store pass can skip its last layer's output")
         ex = self.exchange
         cos, sin = rope.cos_sin(ex.npb, height, width, p.chunk * ex.npb, ex.head_dim, device=x.device)
         ex.prepare_pass(p, height, width)
         es_all = self._modulation.unsqueeze(1) + e.unsqueeze(0)   # [L, F, 6, dim], one bf16 add
         pending = None
+        last = len(self.blocks) - 1
         for L, blk in enumerate(self.blocks):
             pool, ctx, own, n_ctx = ex.layer_context(L, p, height, width)
             ku = ex.anchor_ku_out(L) if p.kind == "store" else None
             # each block's last gated residual runs fused into the next block's first LayerNorm
             x, pending = blk.forward(x, e, cos, sin, pool, ctx, own, n_ctx, self.text_kv[L], unroped_k_out=ku,
-                                     es=es_all[L], pending=pending, defer_residual=True)
+                                     es=es_all[L], pending=pending, defer_residual=True,
+                                     kv_only=kv_only_last and L == last)
+        if kv_only_last:
+            return None
         apply_pending_residual(x, pending, x.shape[0] // e.shape[0])
         return x
 
