@@ -392,7 +392,7 @@ def bench_dit(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
     noisy = torch.randn((1, 16, frames, H, W), generator=g, device=dev).to(torch.bfloat16)
     steps_t = dit.schedule.warp()
     for c in range(8):
-        dit.forward_chunk(noisy, 0.0, c, store=True)
+        dit.forward_chunk(noisy, 0.0, chunk=c, store=True)
     plan = TickPlan(STEADY_TICK, [0, 1, 2, 3], True, (STEADY_TICK - 3) * frames, 4 * frames)
     ex.begin_tick(plan)
     dit.run_pass(noisy, 0.0, ex.store_pass(), want_x0=False)

@@ -230,7 +230,7 @@ def test_store_pass_stops_after_the_last_layers_kv():
     g = torch.Generator().manual_seed(52)
     for c in range(3):
         lat = torch.randn((1, 16, 3, H, W), generator=g).to(BF16).to(DEV)
-        short.forward_chunk(lat, 0.0, c, store=True)
+        short.forward_chunk(lat, 0.0, chunk=c, store=True)
         ex = full.stack.exchange
         ex.begin_tick(TickPlan(c + 4, [], True, 0, 0))
         full.run_pass(lat, 0.0, ex.store_pass(), want_x0=True)
@@ -241,6 +241,10 @@ def test_store_pass_stops_after_the_last_layers_kv():
         assert torch.equal(getattr(a.pool, name), getattr(b.pool, name)), name
     assert torch.equal(a.anchor_ku, b.anchor_ku)
     x0a = short.forward_chunk(noisy.to(DEV), 937.5, chunk=3)
-    x0b = full.forward_chunk(noisy.to(DEV), 937.5, chunk=3)
+    x0b = full.forward_chunk(noisy.to(DEV), 937.5, 9)     # the reference's call: start_frame = 3 chunks x 3
     torch.cuda.synchronize()
     assert torch.equal(x0a, x0b)
+    with pytest.raises(ValueError, match="chunk start"):
+        full.forward_chunk(noisy.to(DEV), 937.5, 4)
+    with pytest.raises(ValueError, match="exactly one"):
+        full.forward_chunk(noisy.to(DEV), 937.5, 9, chunk=3)

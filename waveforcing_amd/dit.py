@@ -292,10 +292,19 @@ class QuantizedWanDiT:
                                  hp, wp, pre=pre, post=post)
         return dict(zip(ranks, x0s))
 
-    def forward_chunk(self, noisy: torch.Tensor, t: float, chunk: int, store: bool = False):
-        """One chunk alone as a tick of its own (backend.py:456-490's call for a single chunk): a store pass
-        (the chunk joins the clean lists; returns None) or a denoise pass of rank 0 (returns x0)."""
+    def forward_chunk(self, noisy: torch.Tensor, t: float, start_frame: int | None = None, *,
+                      chunk: int | None = None, store: bool = False):
+        """One chunk alone as a tick of its own, called like ``WaveBackend.forward_chunk(noisy_chunk_bcthw,
+        step_value, start_frame)`` (backend.py:456-490; ``start_frame`` a multiple of the chunk's frames, or
+        the chunk index as ``chunk=``): a store pass (the chunk joins the clean lists; returns None) or a
+        denoise pass of rank 0 (returns x0 [1, F, 16, H, W], B T C H W)."""
         ex = self.stack.exchange
+        if (start_frame is None) == (chunk is None):
+            raise ValueError("give exactly one of start_frame and chunk")
+        if start_frame is not None:
+            if start_frame < 0 or start_frame % ex.npb:
+                raise ValueError(f"start_frame {start_frame} is not a chunk start (chunks of {ex.npb} frames)")
+            chunk = start_frame // ex.npb
         Fr = noisy.shape[2]
         if store:
             self.tick(TickPlan(chunk + ex.rf_step, [], True, 0, 0), {"store": (noisy, t)})
