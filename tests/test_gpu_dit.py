@@ -248,3 +248,82 @@ def test_store_pass_stops_after_the_last_layers_kv():
         full.forward_chunk(noisy.to(DEV), 937.5, 4)
     with pytest.raises(ValueError, match="exactly one"):
         full.forward_chunk(noisy.to(DEV), 937.5, 9, chunk=3)
+
+
+def test_wavefront_stream_passes_match_the_oracle():
+    """Every denoise pass of a 4-chunk stream at rf_step 2 (WavefrontDenoiser.generate: noise in, re-noised
+    hand-offs between the two DMD steps, store passes at the context noise) against the oracle DiT forward
+    fed the latent and timestep the pass was given, over the reference's context for that pass (the list
+    model of exchange_model: anchor re-RoPEd to the pass's start, working chunks, the live stored chunk,
+    the in-flight chunk of the other rank), with oracle pools filled by the oracle's own store and denoise
+    passes: flow part of x0 within relative L2 1e-2 for every pass."""
+    import exchange_model as em
+    from waveforcing_amd.wavefront import WavefrontDenoiser
+
+    dim, heads, ffn, layers, H, W = 256, 2, 512, 2, 16, 16
+    hp, wp, npb, rf, window, n_chunks = H // 2, W // 2, 3, 2, 15, 4
+    page = hp * wp
+    T = npb * page
+    bparams, dparams, _, ctx = _dit_case(dim, heads, ffn, layers, H, W, seed=61)
+    blocks = [QuantizedWanBlock(p, heads, DEV) for p in bparams]
+    dit = QuantizedWanDiT(dparams, QuantizedWanStack(blocks, PagedExchange(layers, heads, page, npb, window,
+                                                                            rf_step=rf, device=DEV)))
+    dit.set_text(ctx.to(DEV))
+    record = []
+    real_tick = dit.tick
+
+    def spy(plan, inputs, concurrent=False):
+        ins = {k: (lat.detach().cpu().clone(), float(t)) for k, (lat, t) in inputs.items()}
+        out = real_tick(plan, inputs, concurrent=concurrent)
+        record.append((plan, ins, {r: x0.detach().cpu().clone() for r, x0 in out.items()}))
+        return out
+
+    dit.tick = spy
+    noise = torch.randn((1, 16, npb * n_chunks, H, W), generator=torch.Generator().manual_seed(62)).to(BF16)
+    WavefrontDenoiser(dit, steps=(1000, 500)).generate(noise.to(DEV))
+    torch.cuda.synchronize()
+    assert len(record) == n_chunks + rf
+
+    oemb = od.text_embed(dparams, ctx)
+    otext = [ob.text_kv(p, oemb, heads) for p in bparams]
+    sched = FlowMatchSchedule()
+    pk = [okv.new_pool(npb * n_chunks, page, heads, 128) for _ in range(layers)]
+    pv = [okv.new_pool(npb * n_chunks, page, heads, 128) for _ in range(layers)]
+
+    def pages(c):
+        return list(range(npb * c, npb * c + npb))
+
+    clean, anchor_ku, checked, moved = [], [None] * layers, 0, False
+    for plan, ins, outs in record:
+        for r, c, csf, qf in em.passes(plan, rf, npb):
+            lat, t = ins["store" if r == rf else r]
+            anchor, start, ids = em.context(clean, plan, r, csf, qf, window, npb, rf)
+            moved |= anchor is not None and start != anchor * npb
+
+            def stack_fn(xs, e0):
+                x = xs
+                for L, p in enumerate(bparams):
+                    if anchor is not None:
+                        ang = ob.rope_angles(npb, hp, wp, start)
+                        ak = ob.rope_apply_table(anchor_ku[L], torch.cos(ang).float(), torch.sin(ang).float())
+                        okv.pack(ak, pages(anchor), page, *pk[L])
+                    x, ku = ob.block_forward(p, x, e0, (npb, hp, wp), c * npb, pk[L], pv[L],
+                                             [q for i in ids for q in pages(i)], pages(c), len(ids) * T, page,
+                                             *otext[L], heads, return_unroped_k=True)
+                    if r == rf and not clean:
+                        anchor_ku[L] = ku
+                return x
+
+            want = od.dit_forward(dparams, stack_fn, lat[0], t, od.sigma_x0(sched.sigmas, sched.timesteps, t)).double()
+            if r == rf:
+                continue
+            got = outs[r][0].double()
+            xt = lat[0].permute(1, 0, 2, 3).double()
+            rel = (((got - xt) - (want - xt)).norm() / (want - xt).norm()).item()
+            print(f"tick {plan.tick} rank {r} chunk {c} t={t:.1f}: {len(ids)} context chunks, flow rel L2 {rel:.2e}")
+            assert rel <= 1e-2
+            checked += 1
+        if plan.store_active:
+            clean = em.keep_last(clean + [plan.tick - rf])
+    assert checked == n_chunks * rf
+    assert moved

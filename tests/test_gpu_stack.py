@@ -22,6 +22,7 @@ each tick runs the store rank's pass and the active denoise ranks' passes.
 import pytest
 import torch
 
+import exchange_model as em
 from oracle import block as ob
 from oracle import kv as okv
 from waveforcing_amd import exchange as ex
@@ -70,28 +71,14 @@ def _pages(c):
 
 
 def _passes(plan):
-    """(rank, chunk, csf, qf) of a tick's passes in execution order; rank RF is the store rank."""
-    out = [(RF, plan.tick - RF, (plan.tick - RF) * NPB, NPB)] if plan.store_active else []
-    return out + [(r, plan.tick - r, plan.csf, plan.qf) for r in sorted(plan.act_ranks, reverse=True)]
+    return em.passes(plan, RF, NPB)
 
 
 def _context(clean, plan, rank, csf, qf):
-    """List model: (anchor chunk or None, its rope start, context chunk ids in the reference's order)."""
-    anchor, start, ids = None, None, []
-    if clean:
-        _, n_w = ex.anchor_and_working(len(clean), ex.working_chunks(WINDOW, qf, NPB))
-        working = clean[len(clean) - n_w:] if n_w else []
-        anchor, start = clean[0], ex.anchor_rope_start(csf, len(working), NPB)
-        ids = [anchor] + working
-    if rank == RF:
-        return anchor, start, ids + [plan.tick - RF]
-    if plan.store_active:
-        ids.append(plan.tick - RF)
-    return anchor, start, ids + [plan.tick - n for n in ex.inflight_order(rank, plan.act_ranks)]
+    return em.context(clean, plan, rank, csf, qf, WINDOW, NPB, RF)
 
 
-def _keep_last(clean):
-    return clean[:1] + clean[-7:] if len(clean) > 8 else clean
+_keep_last = em.keep_last
 
 
 def test_stack_ticks_equal_manual_replay():
