@@ -187,3 +187,24 @@ def test_module_swap_scopes():
     assert quantize_transformer_w8a8(t2, scope="all") == 6
     with pytest.raises(ValueError):
         quantize_transformer_w8a8(torch.nn.Linear(4, 4))
+
+
+@pytest.mark.parametrize("M,N,K,pad,offset", [
+    (700, 512, 256, 16, 0),     # rows strided by N + 16, 16-byte aligned: full 16-byte stores
+    (700, 512, 256, 12, 4),     # an 8-byte-aligned view with an odd row stride: 8-byte stores
+    (300, 1540, 128, 20, 4),    # N % 8 == 4 inside a strided view, one K step
+])
+def test_gemm_into_strided_views(M, N, K, pad, offset):
+    """y written into a column window of a wider matrix (ldy > N, possibly 8-byte aligned only): equal to the
+    oracle inside the window, the columns around it untouched."""
+    x = inputs.outlier_activations(M, K, seed=N, chan_seed=N + 1)
+    w, b = inputs.linear_weights(N, K, w_seed=N + 2, b_seed=N + 3)
+    qx, sx = olin.i8_quant_rows(x)
+    qw, sw = olin.i8_quant_rows(w)
+    big = torch.full((M, N + pad), 7.0, dtype=torch.bfloat16, device=DEV)
+    view = big[:, offset:offset + N]
+    gemm_i8(qx.to(DEV), qw.to(DEV), sx.to(DEV), sw.to(DEV), b.to(DEV), out=view)
+    oy, _ = olin.i8_gemm(qx, qw, sx, sw, b)
+    got = big.cpu()
+    assert torch.equal(got[:, offset:offset + N], oy)
+    assert bool((got[:, :offset] == 7.0).all()) and bool((got[:, offset + N:] == 7.0).all())
