@@ -66,3 +66,13 @@ def test_fp8_pertensor_argument_errors():
         _lib.call("wf_gemm_fp8_pertensor", 16, 32, 4, 4, 24, 48, 64, None, 80, 4, None)
     with pytest.raises(RuntimeError, match="null pointer"):
         _lib.call("wf_fp8_linear_pertensor", 16, 4, 32, 32, 48, 64, None, 8, 80, 8, 96, None, 112, None)
+
+
+def test_row_kernels_refuse_launches_beyond_2_to_32_threads():
+    with pytest.raises(RuntimeError, match="too large"):
+        _lib.call("wf_gate_residual", 16, 1536, 32, 1536, None, 0, 1 << 40, 1536, 4680, None)
+    with pytest.raises(RuntimeError, match="too large"):
+        _lib.call("wf_rmsnorm_rope", 16, 1 << 24, 1536, 1536, 128, 1e-6, 48, None, None, 64, 1536, None)
+    with pytest.raises(RuntimeError, match="too large"):
+        _lib.call("wf_ln_modulate_quant", 16, 1 << 24, 1536, 1536, 1e-6, None, None, None, None, 0, 4680, 32, 1536,
+                  None, None, None)

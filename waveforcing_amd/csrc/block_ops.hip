@@ -299,6 +299,8 @@ int wf_gate_residual_ln_quant(void* x, int64_t T, int32_t dim, int64_t ldx, cons
   static const char* fn = "wf_gate_residual_ln_quant";
   WF_REQUIRE(T >= 0 && dim > 0 && ldx >= dim && frame_tokens > 0, WF_E_INVALID, "%s: bad sizes", fn);
   WF_REQUIRE(dim % 8 == 0 && dim <= 16384, WF_E_SHAPE, "%s: dim=%d (need %% 8 == 0, <= 16384)", fn, dim);
+  WF_REQUIRE(T < (1ll << 24), WF_E_SHAPE, "%s: T=%lld too large (a launch holds at most 2^32 threads)", fn,
+             (long long)T);
   if (T == 0) return WF_OK;
   WF_REQUIRE(x && (out || q), WF_E_INVALID, "%s: null input or no output", fn);
   WF_REQUIRE(!y || ldy >= dim, WF_E_INVALID, "%s: ldy < dim", fn);
@@ -334,6 +336,8 @@ int wf_rmsnorm_rope(const void* x, int64_t T, int32_t dim, int64_t ldx, int32_t 
   WF_REQUIRE(T >= 0 && dim > 0 && head_dim > 0 && ldx >= dim && ldo >= dim, WF_E_INVALID, "%s: bad sizes", fn);
   WF_REQUIRE(dim % 8 == 0 && dim <= 16384 && dim % head_dim == 0 && head_dim % 8 == 0, WF_E_SHAPE,
              "%s: dim=%d head_dim=%d unsupported", fn, dim, head_dim);
+  WF_REQUIRE(T < (1ll << 24), WF_E_SHAPE, "%s: T=%lld too large (a launch holds at most 2^32 threads)", fn,
+             (long long)T);
   if (T == 0) return WF_OK;
   WF_REQUIRE(x && w && out && ((cos == nullptr) == (sin == nullptr)), WF_E_INVALID, "%s: null pointer", fn);
   WF_REQUIRE(wf::a16(x) && wf::a16(w) && wf::a16(out) && ldx % 8 == 0 && ldo % 8 == 0 &&
@@ -365,6 +369,8 @@ int wf_gate_residual(void* x, int64_t ldx, const void* y, int64_t ldy, const voi
   WF_REQUIRE(T >= 0 && dim > 0 && ldx >= dim && ldy >= dim && frame_tokens > 0, WF_E_INVALID, "%s: bad sizes", fn);
   WF_REQUIRE(!gate || ld_gate >= dim, WF_E_INVALID, "%s: ld_gate < dim", fn);
   WF_REQUIRE(dim % 8 == 0, WF_E_SHAPE, "%s: dim %% 8 != 0", fn);
+  WF_REQUIRE(T * (dim / 8) < (1ll << 32) - 256, WF_E_SHAPE, "%s: T=%lld too large (a launch holds at most 2^32 threads)",
+             fn, (long long)T);
   if (T == 0) return WF_OK;
   WF_REQUIRE(x && y, WF_E_INVALID, "%s: null pointer", fn);
   WF_REQUIRE(wf::a16(x) && wf::a16(y) && (!gate || (wf::a16(gate) && ld_gate % 8 == 0)) && ldx % 8 == 0 &&
