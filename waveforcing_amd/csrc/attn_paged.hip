@@ -34,7 +34,7 @@
 // tile is peeled for the masking of keys past n_kv, tiles past the end load
 // as zeros into the stage nobody reads any more):
 //   * the 16 K fragments are read first, then the 16 score MFMAs alternate
-//     with the next tile's dequantization (sched_group_barrier: 1 MFMA, 5
+//     with the next tile's dequantization (sched_group_barrier: 1 MFMA, 4
 //     VALU), whose result is then written to the other stage;
 //   * the 32 V^T reads are issued before the softmax, so they land during it;
 //   * each 16-key step's exponentials feed its 4 PV MFMAs, so the
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // then 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // and 5 VALU, alternating
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // and 4 VALU, alternating
     }
     // the next tile into the other stage (freed by the last barrier), the
     // loads of the one after, and this tile's V^T operands (in flight
