@@ -282,7 +282,8 @@ int wf_fp8_linear_pertensor(const void* x, int64_t m, int64_t k, int64_t ldx,
  *   out[q,h,:] = softmax_j(softmax_scale * <q[q,h,:], K[j,h,:]>) . V[j,h,:]
  * with K = code_k * s_k and V = code_v * s_v per (key, head); fp32
  * accumulation, bf16 out [lq][n_heads][128] (token stride ldo).
- * page_tokens >= 64; each code pool < 2 GiB.  Replaces the attention
+ * page_tokens >= 64; each code pool < 2 GiB.  n_kv == 0 writes zero rows
+ * (the pools may then be NULL).  Replaces the attention
  * dispatch of the patched self-attention (wave_rt/runtime/backend.py:141-148:
  * fa_func / sageattn / SDPA over the paged context views of
  * wave_rt/denoiser/exchange/paged.py:246-247). */

@@ -15,7 +15,7 @@ import torch
 
 from oracle import attention as oat
 from oracle import kv as okv
-from waveforcing_amd import inputs
+from waveforcing_amd import _lib, inputs
 from waveforcing_amd.backend import _WAVE_STATE, attend, attn_dense_bf16, attn_paged_fp8, enable_hip_fp8
 from waveforcing_amd.kv import Fp8PagePool, PagedKV
 
@@ -142,3 +142,40 @@ def test_backend_dispatch_and_scale():
     finally:
         _WAVE_STATE.clear()
         _WAVE_STATE.update(saved)
+
+
+def test_empty_context_writes_zeros():
+    """n_kv = 0: an empty softmax gives every query zero weight, so the output rows are zeros (no pools are
+    read; null pool pointers are accepted)."""
+    H, Lq = 2, 70
+    q = _normal((Lq, H, 128), 70).to(DEV)
+    out = torch.full((Lq, H, 128), 7.0, dtype=torch.bfloat16, device=DEV)
+    _lib.call("wf_attn_paged_fp8", q.data_ptr(), Lq, H, 128, H * 128, None, None, None, None, 0, 64, None, 0, 0,
+              128 ** -0.5, out.data_ptr(), H * 128, _lib.stream_handle(DEV))
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0
+
+
+def test_page_ids_outside_the_pool_read_as_zero_keys():
+    """A page-table entry outside [0, pool_pages) is never read: its keys enter the softmax with K = 0
+    (score 0) and V = 0, as include/wf_api.h states.  Raw C call (the Python PageTable refuses such ids)."""
+    H, Lq, page, n_kv, P = 2, 100, 64, 3 * 64 - 10, 5
+    q, pool, ctx, ids, kp, vp, _ = _setup(Lq, H, n_kv, page, P, seed=80)
+    table = torch.tensor([ids[0], -1, P + 3], dtype=torch.int32, device=DEV)
+    out = torch.empty((Lq, H, 128), dtype=torch.bfloat16, device=DEV)
+    qd = q.to(DEV)
+    _lib.call("wf_attn_paged_fp8", qd.data_ptr(), Lq, H, 128, H * 128, pool.k_codes.data_ptr(),
+              pool.v_codes.data_ptr(), pool.k_scales.data_ptr(), pool.v_scales.data_ptr(), P, page,
+              table.data_ptr(), 3, n_kv, 128 ** -0.5, out.data_ptr(), H * 128, _lib.stream_handle(DEV))
+    torch.cuda.synchronize()
+    k = okv.unpack(ids, n_kv, page, *kp)
+    v = okv.unpack(ids, n_kv, page, *vp)
+    k[page:] = 0
+    v[page:] = 0
+    ref = oat.sdpa(q, k, v)
+    err = (out.cpu().float() - ref).abs().max().item()
+    print(f"max abs err {err:.3e}")
+    assert err <= TOL, err
+    # and the zero keys do weigh in: attending to the valid page alone differs
+    alone = oat.sdpa(q, k[:page], v[:page])
+    assert (alone - ref).abs().max().item() > 10 * TOL
