@@ -173,3 +173,37 @@ def test_gate_residual_strided_gate():
     torch.cuda.synchronize()
     fr = torch.arange(T) // ft
     assert torch.equal(xd.cpu(), x + y * es[fr, 5])
+
+
+@pytest.mark.parametrize("dim", [64, 1536, 2056, 5120, 13824])
+@pytest.mark.parametrize("form", ["gated_mod", "mod", "plain_res_mod", "gated_affine"])
+def test_ln_forms_match_the_general_kernel(dim, form):
+    """The LayerNorm launches of the block (int8 output only) run kernels specialized at compile time;
+    the same call with a bf16 output as well runs the run-time form.  Codes, scales and the in-place
+    residual must agree bit for bit."""
+    g = torch.Generator().manual_seed(7 * dim + len(form))
+    F, ft = 3, 20
+    T = F * ft
+    x = torch.randn((T, dim), generator=g).to(torch.bfloat16).to(DEV)
+    y = torch.randn((T, dim), generator=g).to(torch.bfloat16).to(DEV)
+    es = _mod_rows(F, dim, g).to(DEV)
+    w = (1 + 0.05 * torch.randn((dim,), generator=g)).to(torch.bfloat16).to(DEV)
+    b = (0.01 * torch.randn((dim,), generator=g)).to(torch.bfloat16).to(DEV)
+    res_y = None if form == "mod" else y
+    gate = es[:, 2] if form.startswith("gated") else None
+    aff = form == "gated_affine"
+    shift, scale = (None, None) if aff else (es[:, 0], es[:, 1])
+    ld = es.stride(0)
+    got = []
+    for with_out in (False, True):
+        xd = x.clone()
+        q = torch.empty((T, dim), dtype=torch.int8, device=DEV)
+        qs = torch.empty((T,), dtype=torch.float32, device=DEV)
+        out = torch.empty((T, dim), dtype=torch.bfloat16, device=DEV) if with_out else None
+        _lib.call("wf_gate_residual_ln_quant", xd.data_ptr(), T, dim, dim, _lib.ptr(res_y), dim, _lib.ptr(gate), ld,
+                  EPS, _lib.ptr(w) if aff else None, _lib.ptr(b) if aff else None, _lib.ptr(shift), _lib.ptr(scale),
+                  ld, ft, _lib.ptr(out), dim if with_out else 0, q.data_ptr(), qs.data_ptr(), _lib.stream_handle(DEV))
+        got.append((xd, q, qs))
+    torch.cuda.synchronize()
+    (x0, q0, s0), (x1, q1, s1) = got
+    assert torch.equal(x0, x1) and torch.equal(q0, q1) and torch.equal(s0, s1)

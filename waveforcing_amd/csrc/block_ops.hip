@@ -36,13 +36,41 @@ struct LnArgs {
   float* qs;               // fp32 [T] (with q)
 };
 
+// Which operands a launch has.  Form 0 reads that from the null-ness of LnArgs' pointers at run time
+// (every combination); the others fix it at compile time for the block's norms, so their kernels carry
+// no branches on it (the same operations in the same order: bit-identical to form 0).
+struct LnForm {
+  int res;    // 0: no residual, 1: x + y, 2: x + y * gate
+  bool mod;   // shift and scale modulation
+  bool aff;   // affine weight and bias
+  bool out;   // bf16 output
+  bool q;     // int8 output
+};
+constexpr LnForm kLnForms[] = {
+    {0, false, false, false, false},  // 0: run-time
+    {2, true, false, false, true},    // 1: LN1 after the previous block's gated residual, modulation, int8
+    {0, true, false, false, true},    // 2: LN1 of a stack's first block
+    {1, true, false, false, true},    // 3: cross-attention residual + LN2, modulation, int8
+    {2, false, true, false, true},    // 4: self-attention gated residual + norm3 (affine), int8
+};
+constexpr int kNumLnForms = sizeof(kLnForms) / sizeof(kLnForms[0]);
+
 // [x = bf16(x + bf16(ry * rgate[f]))  or  x = bf16(x + ry)]   (causal_model.py:386,390,397-398)
 // y = LN(x) [* w + b]  (fp32 statistics, rounded to bf16: WanLayerNorm, model.py:89-99)
 // y = bf16(bf16(y * bf16(1 + e_b)) + e_a)                     (causal_model.py:381,393-394)
 // optional bf16 output and per-token int8 quantization of y.
-template <int LPR, int NC>
+template <int LPR, int NC, int FORM>
 __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
   constexpr int RPB = 256 / LPR;
+  constexpr LnForm F = kLnForms[FORM];
+  const bool has_ry = FORM ? F.res > 0 : a.ry != nullptr;
+  const bool has_gate = FORM ? F.res == 2 : a.rgate != nullptr;
+  const bool has_shift = FORM ? F.mod : a.shift != nullptr;
+  const bool has_scale = FORM ? F.mod : a.scale != nullptr;
+  const bool has_w = FORM ? F.aff : a.w != nullptr;
+  const bool has_b = FORM ? F.aff : a.b != nullptr;
+  const bool has_out = FORM ? F.out : a.out != nullptr;
+  const bool has_q = FORM ? F.q : a.q != nullptr;
   __shared__ float red[3][4];
   const int lane = static_cast<int>(threadIdx.x) % LPR;
   const int t = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / LPR;
@@ -54,7 +82,7 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
   // The row is kept as packed bf16 (4 registers per chunk) and unpacked in
   // each pass; the affine and modulation rows are fetched with the row, so
   // every load is in flight before the first reduction.
-  const bool mod = a.shift || a.scale;
+  const bool mod = has_shift || has_scale;
   uint4 xr[NC], pa[NC], pb[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
@@ -62,14 +90,14 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
     const bool ok = ch < n_chunks;
     const uint4 z = make_uint4(0, 0, 0, 0);
     xr[c] = ok ? ld16(row + ch * 8) : z;
-    if (a.ry) {
+    if (has_ry) {
       uint4 yr = ok ? ld16(a.ry + static_cast<int64_t>(t) * a.ldry + ch * 8) : z;
-      uint4 gr = a.rgate && ok ? ld16(a.rgate + static_cast<int64_t>(f) * a.ld_rgate + ch * 8) : z;
+      uint4 gr = has_gate && ok ? ld16(a.rgate + static_cast<int64_t>(f) * a.ld_rgate + ch * 8) : z;
       // residual, applied as soon as its operands arrive
       float v[8], y[8];
       unpack8(xr[c], v);
       unpack8(yr, y);
-      if (a.rgate) {
+      if (has_gate) {
         float g[8];
         unpack8(gr, g);
 #pragma unroll
@@ -83,11 +111,11 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
     }
     // pa/pb: (shift, scale) of the modulation if there is one, else the affine (w, b)
     if (mod) {
-      if (a.shift) pa[c] = ok ? ld16(a.shift + static_cast<int64_t>(f) * a.ld_mod + ch * 8) : z;
-      if (a.scale) pb[c] = ok ? ld16(a.scale + static_cast<int64_t>(f) * a.ld_mod + ch * 8) : z;
+      if (has_shift) pa[c] = ok ? ld16(a.shift + static_cast<int64_t>(f) * a.ld_mod + ch * 8) : z;
+      if (has_scale) pb[c] = ok ? ld16(a.scale + static_cast<int64_t>(f) * a.ld_mod + ch * 8) : z;
     } else {
-      if (a.w) pa[c] = ok ? ld16(a.w + ch * 8) : z;
-      if (a.b) pb[c] = ok ? ld16(a.b + ch * 8) : z;
+      if (has_w) pa[c] = ok ? ld16(a.w + ch * 8) : z;
+      if (has_b) pb[c] = ok ? ld16(a.b + ch * 8) : z;
     }
   }
   float sum = 0.f;
@@ -123,20 +151,20 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
       unpack8(xr[c], v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) y[i] = (v[i] - mean) * rstd;
-      if (a.w) {
+      if (has_w) {
         float wv[8];
         unpack8(mod ? ld16(a.w + ch * 8) : pa[c], wv);
 #pragma unroll
         for (int i = 0; i < 8; ++i) y[i] = y[i] * wv[i];
       }
-      if (a.b) {
+      if (has_b) {
         float bv[8];
         unpack8(mod ? ld16(a.b + ch * 8) : pb[c], bv);
 #pragma unroll
         for (int i = 0; i < 8; ++i) y[i] = y[i] + bv[i];
       }
       rbf8(y);
-      if (a.scale) {
+      if (has_scale) {
         float sc[8];
         unpack8(pb[c], sc);
 #pragma unroll
@@ -146,7 +174,7 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
         for (int i = 0; i < 8; ++i) y[i] = y[i] * sc[i];
         rbf8(y);
       }
-      if (a.shift) {
+      if (has_shift) {
         float sh[8];
         unpack8(pa[c], sh);
 #pragma unroll
@@ -156,10 +184,10 @@ __global__ __launch_bounds__(256) void ln_mod_quant_kernel(LnArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(y[i]));
       xr[c] = pack8(y);
-      if (a.out) st16(a.out + static_cast<int64_t>(t) * a.ldo + ch * 8, xr[c]);
+      if (has_out) st16(a.out + static_cast<int64_t>(t) * a.ldo + ch * 8, xr[c]);
     }
   }
-  if (a.q) {
+  if (has_q) {
     amax = row_max_nonneg<LPR>(amax, red[2]);
     const float s = i8_scale(amax);
     const double rd = i8_recip(s);
@@ -280,10 +308,25 @@ int launch_ln(const LnArgs& a, hipStream_t stream, const char* fn) {
   int lpr = 0, nc = 0;
   pick_shape(a.dim / 8, lpr, nc);
   const uint32_t grid = static_cast<uint32_t>((a.T + 256 / lpr - 1) / (256 / lpr));
+  const LnForm have{a.ry ? (a.rgate ? 2 : 1) : 0, a.shift && a.scale, a.w && a.b, a.out != nullptr,
+                    a.q != nullptr};
+  const bool partial = (!a.shift != !a.scale) || (!a.w != !a.b) || (have.mod && have.aff);
+  int form = 0;
+  for (int i = 1; i < kNumLnForms && !partial; ++i) {
+    const LnForm& f = kLnForms[i];
+    if (f.res == have.res && f.mod == have.mod && f.aff == have.aff && f.out == have.out && f.q == have.q) form = i;
+  }
   dispatch_shape(lpr, nc, [&](auto L, auto C) {
-    hipLaunchKernelGGL((ln_mod_quant_kernel<decltype(L)::value, decltype(C)::value>), dim3(grid), dim3(256), 0,
-                       stream, a);
+    constexpr int l = decltype(L)::value, c = decltype(C)::value;
+    switch (form) {
+      case 1: hipLaunchKernelGGL((ln_mod_quant_kernel<l, c, 1>), dim3(grid), dim3(256), 0, stream, a); break;
+      case 2: hipLaunchKernelGGL((ln_mod_quant_kernel<l, c, 2>), dim3(grid), dim3(256), 0, stream, a); break;
+      case 3: hipLaunchKernelGGL((ln_mod_quant_kernel<l, c, 3>), dim3(grid), dim3(256), 0, stream, a); break;
+      case 4: hipLaunchKernelGGL((ln_mod_quant_kernel<l, c, 4>), dim3(grid), dim3(256), 0, stream, a); break;
+      default: hipLaunchKernelGGL((ln_mod_quant_kernel<l, c, 0>), dim3(grid), dim3(256), 0, stream, a); break;
+    }
   });
+  static_assert(kNumLnForms == 5, "one launch case per form");
   return check_launch(fn);
 }
 
