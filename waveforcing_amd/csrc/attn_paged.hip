@@ -425,21 +425,28 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
     body(n_tiles - 1, std::true_type{});
   }
 
-  // normalize and store: lane's query q, d = 32*db + 8*(r/4) + 4*half + r%4
+  // normalize, stage through LDS as bf16 [query][d] rows (every wave its own 32 rows; the last
+  // tile's barrier has retired every read of the stages), then store 256-byte row segments.
   const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  const int q = q0 + wave * 32 + l32;
-  if (q < p.Lq) {
-    uint16_t* op = p.out + static_cast<int64_t>(q) * p.ldo + h * D + half * 4;
+  constexpr int OPITCH = D * 2 + 8;  // staged row pitch (bytes)
+  static_assert(WAVES * 32 * OPITCH <= 2 * STAGE, "output staging fits the stages");
+  uint8_t* ow = lds + wave * 32 * OPITCH;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+  for (int db = 0; db < 4; ++db) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const uint2 w = make_uint2(cvt_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
-                                   cvt_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv));
-        *reinterpret_cast<uint2*>(op + db * 32 + g * 8) = w;
-      }
+    for (int g = 0; g < 4; ++g) {
+      const uint2 w = make_uint2(cvt_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
+                                 cvt_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv));
+      *reinterpret_cast<uint2*>(ow + l32 * OPITCH + 64 * db + 16 * g + 8 * half) = w;
     }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 2 * i + half;
+    const uint2 w = *reinterpret_cast<const uint2*>(ow + row * OPITCH + 8 * l32);
+    const int qr = q0 + wave * 32 + row;
+    if (qr < p.Lq) *reinterpret_cast<uint2*>(p.out + static_cast<int64_t>(qr) * p.ldo + h * D + 4 * l32) = w;
   }
 }
 
