@@ -98,29 +98,37 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_bf16_kernel(Bf16GemmArgs p) 
     w0 = w0n;
     w1 = w1n;
   }
-  // lane's row m = m0 + l32; register r of block j is column n0 + 32 j + 8 (r / 4) + 4 half + r % 4
-  const int m = m0 + l32;
-  if (m >= p.M) return;
-  uint16_t* yrow = p.y + static_cast<int64_t>(m) * p.ldy;
+  // lane's row m0 + l32; register r of block j is column n0 + 32 j + 8 (r / 4) + 4 half + r % 4.  The
+  // wave's 32 x 64 results go through its own LDS rows, so each row is stored as one 128-byte segment.
+  constexpr int YP = 64 * 2 + 8;  // staged row pitch (bytes)
+  __shared__ __attribute__((aligned(16))) uint8_t ys[kWaves * 32 * YP];
+  uint8_t* yw = ys + wave * 32 * YP;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const v16f& acc = j == 0 ? acc0 : acc1;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = n0 + 32 * j + 8 * g + 4 * half;
-      if (n >= p.N) continue;
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float t = acc[4 * g + e];
-        if (p.bias) t = __fadd_rn(t, bf16_bits_to_f32(p.bias[n + e]));
+        if (p.bias && n < p.N) t = __fadd_rn(t, bf16_bits_to_f32(p.bias[n + e]));
         t = bf16_round(t);
         if constexpr (ACT_OUT == 1) t = silu(t);
         if constexpr (ACT_OUT == 2) t = gelu_tanh(t);
         v[e] = t;
       }
-      *reinterpret_cast<uint2*>(yrow + n) = make_uint2(pack_bf16x2_hw(v[0], v[1]), pack_bf16x2_hw(v[2], v[3]));
+      *reinterpret_cast<uint2*>(yw + l32 * YP + 2 * (32 * j + 8 * g + 4 * half)) =
+          make_uint2(pack_bf16x2_hw(v[0], v[1]), pack_bf16x2_hw(v[2], v[3]));
     }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 4 * i + (lane >> 4);
+    const int m = m0 + row, n = n0 + 4 * (lane & 15);
+    const uint2 w = *reinterpret_cast<const uint2*>(yw + row * YP + 8 * (lane & 15));
+    if (m < p.M && n < p.N) *reinterpret_cast<uint2*>(p.y + static_cast<int64_t>(m) * p.ldy + n) = w;
   }
 }
 
