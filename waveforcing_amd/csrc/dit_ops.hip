@@ -23,8 +23,9 @@
 // operand fragments of that MFMA are 16 contiguous bytes of one row of A
 // and of W (lane l: row l % 32, K elements 8 (l / 32) .. + 7), so they are
 // loaded straight from global memory (neighbouring K steps share cache
-// lines), one K step ahead of the MFMAs.  These GEMMs are a few percent of
-// a chunk's work (0.9 GFLOP for the patch embedding or the head at 1.3B).
+// lines), one K step ahead of the MFMAs.  Each wave's results go out through
+// its own LDS rows as 128-byte row segments.  These GEMMs are a few percent
+// of a chunk's work (0.9 GFLOP for the patch embedding or the head at 1.3B).
 #include <type_traits>
 
 #include "wf_common.hpp"
