@@ -1,5 +1,5 @@
-"""The Wan DiT's layers around the blocks (torch CPU), test infrastructure only: the checker of
-waveforcing_amd.dit.
+"""The Wan DiT's layers around the blocks (torch CPU), test infrastructure only: what
+waveforcing_amd.dit is tested against.
 
 Restates, in the dtypes the reference runs them (a bf16 model; the autocast
 blocks are commented out, causal_model.py:841,871):

@@ -1,6 +1,6 @@
 """Flow-matching schedule and deterministic re-noising oracle (torch CPU).
 
-Test infrastructure only: the checker of waveforcing_amd.schedule.
+Test infrastructure only: what waveforcing_amd.schedule is tested against.
 
 * Sigma / timestep table of FlowMatchScheduler.set_timesteps
   (naive_rt/rolling_forcing/utils/scheduler.py:108-136) with the generator's
