@@ -56,6 +56,10 @@ def _setup(Lq, H, n_kv, page, P, seed, const_v=False, heavy=False):
     (130, 3, 64, 64, 2, 1),              # single tile, query tail
     (128, 12, 4680, 1560, 6, 2),         # one 1.3B chunk of context
     (257, 5, 1000, 1560, 3, 3),          # partial page
+    (1, 1, 1, 64, 1, 4),                 # one query, one key
+    (33, 2, 63, 64, 2, 5),               # one partial tile
+    (65, 2, 65, 64, 3, 6),               # one key past the first tile, on the second page
+    (512, 4, 128, 64, 4, 7),             # two full query tiles, two full key tiles, page = tile
 ])
 def test_paged_attention_matches_oracle(Lq, H, n_kv, page, P, seed):
     q, pool, ctx, ids, kp, vp, _ = _setup(Lq, H, n_kv, page, P, seed)
@@ -123,6 +127,16 @@ def test_constant_v_returns_v():
     cv, sv = okv.quantize_rows(v[:1])
     vrow = okv.dequantize_rows(cv, sv).float()
     assert (out - vrow.expand_as(out)).abs().max().item() <= 1e-2
+
+
+def test_single_key_returns_its_value_exactly():
+    """One key: its weight is 2^0 rounded to bf16 (1.0) and the row sum 1, the masked keys weigh 0, so
+    every query's output row is that key's dequantized V, bf16(code * scale), bit for bit."""
+    q, pool, ctx, ids, kp, vp, v = _setup(70, 3, 1, 64, 2, seed=40)
+    out = attn_paged_fp8(q.to(DEV), ctx).cpu()
+    cv, sv = okv.quantize_rows(v[:1])
+    vrow = okv.dequantize_rows(cv, sv)
+    assert torch.equal(out, vrow.expand_as(out))
 
 
 def test_backend_dispatch_and_scale():
