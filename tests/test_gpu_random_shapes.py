@@ -1,12 +1,14 @@
-"""Seeded random shapes for the paged FP8 KV kernels against the CPU oracle.
+"""Seeded random shapes for the KV kernels and the W8A8 GEMM against the CPU oracle.
 
 The pack and the gather-dequant must match bit for bit, and the paged attention must stay within
-max |out - oracle| <= 2e-2 (Q, K, V ~ N(0, 1), as in the attention parity tests). The shapes are
+max |out - oracle| <= 2e-2 (Q, K, V ~ N(0, 1), as in the attention parity tests). The KV shapes are
 drawn across the ranges the kernels take:
 - token counts that are not a multiple of any block size;
 - pages of 16 tokens or more for the pack, 64 or more for attention;
 - 1 to 40 heads;
 - shuffled page tables over pools with unused pages.
+The int8 GEMM must give the oracle's int32 accumulators and bf16 outputs bit for bit over random
+M, N (a multiple of 4) and K (a multiple of 16), with and without bias.
 """
 
 import numpy as np
@@ -15,8 +17,10 @@ import torch
 
 from oracle import attention as oat
 from oracle import kv as okv
+from oracle import linear as olin
 from waveforcing_amd import inputs
 from waveforcing_amd.backend import attn_paged_fp8
+from waveforcing_amd.fp8 import gemm_i8
 from waveforcing_amd.kv import Fp8PagePool, PagedKV
 
 pytestmark = pytest.mark.gpu
@@ -89,3 +93,23 @@ def test_random_paged_attention(Lq, H, n_kv, page, P, seed):
     err = (out.float() - ref).abs().max().item()
     print(f"max abs err {err:.3e}")
     assert err <= TOL, err
+
+
+def _gemm_shapes(n, seed):
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 2500)), 4 * int(rng.integers(1, 1000)), 16 * int(rng.integers(1, 256)),
+             bool(rng.integers(0, 2)), 1000 * seed + i) for i in range(n)]
+
+
+@pytest.mark.parametrize("M,N,K,bias,seed", _gemm_shapes(12, seed=7))
+def test_random_gemm_i8_exact(M, N, K, bias, seed):
+    print(f"gemm M={M} N={N} K={K} bias={bias} seed={seed}", flush=True)
+    x = inputs.outlier_activations(M, K, seed=seed, chan_seed=seed + 1)
+    w, b = inputs.linear_weights(N, K, w_seed=seed + 2, b_seed=seed + 3)
+    qx, sx = olin.i8_quant_rows(x)
+    qw, sw = olin.i8_quant_rows(w)
+    acc = torch.empty((M, N), dtype=torch.int32, device=DEV)
+    y = gemm_i8(qx.to(DEV), qw.to(DEV), sx.to(DEV), sw.to(DEV), b.to(DEV) if bias else None, acc_out=acc)
+    oy, oacc = olin.i8_gemm(qx, qw, sx, sw, b if bias else None)
+    assert torch.equal(acc.cpu(), oacc)
+    assert torch.equal(y.cpu(), oy)
