@@ -7,6 +7,10 @@
   exponential differs from the CPU's, relative L2 <= 1e-3;
 * patch gather: bit-exact;
 * unpatchify + flow -> x0: bit-exact (float64 arithmetic, float32 route to bf16);
+* the time and text embeddings of QuantizedWanDiT with the one-hot probes of
+  tests/embed_probes.py: within one bf16 ulp of the float64 definitions of
+  their SiLU / GELU(tanh) activations, the text padding rows equal to the
+  second bias bit for bit;
 * one chunk's whole forward (QuantizedWanDiT.forward_chunk: patch embedding,
   time embedding, 2 blocks over the paged exchange, head, x0) against the
   oracle chained over the same parameters, at a small width and at the 1.3B
@@ -16,6 +20,7 @@
 import pytest
 import torch
 
+import embed_probes as ep
 from oracle import block as ob
 from oracle import dit as od
 from oracle import kv as okv
@@ -79,6 +84,31 @@ def test_unpatchify_flow_x0_exact(sigma):
               float(sigma), x0.data_ptr(), _lib.stream_handle(DEV))
     want = od.flow_to_x0(od.unpatchify(head, (3, 30, 52)), xt[0], sigma).permute(1, 0, 2, 3)
     assert torch.equal(x0.cpu()[0], want)
+
+
+def _probe_dit(dparams, dim=256, heads=2, ffn=512):
+    blocks = [QuantizedWanBlock(random_block_params(dim, ffn, seed=1), heads, DEV)]
+    stack = QuantizedWanStack(blocks, PagedExchange(1, heads, 64, 3, 21, rf_step=4, device=DEV))
+    return QuantizedWanDiT(dparams, stack)
+
+
+@pytest.mark.parametrize("t", [1000.0, 937.5, 625.0, 3.0])
+def test_time_embedding_probe_closed_form(t):
+    p, picks = ep.time_probe(random_dit_params(256, seed=9))
+    e, e0 = _probe_dit(p).time_modulation(t, 3)
+    want_e, want_e0 = ep.time_closed_form(t, 3, picks)
+    print(f"e exact {(e.cpu() == want_e).double().mean().item():.4f}, "
+          f"e0 exact {(e0.cpu() == want_e0).double().mean().item():.4f}")
+    assert ep.within_one_ulp(e.cpu(), want_e) and ep.within_one_ulp(e0.cpu(), want_e0)
+
+
+def test_text_embedding_probe_closed_form():
+    p, ctx, picks = ep.text_probe(random_dit_params(256, seed=10))
+    got = _probe_dit(p).set_text(ctx.to(DEV)).cpu()
+    want = ep.text_closed_form(ctx, p.text2_b, picks)
+    print(f"exact {(got == want).double().mean().item():.4f}")
+    assert ep.within_one_ulp(got, want)
+    assert torch.equal(got[ctx.shape[0]:], p.text2_b.expand(512 - ctx.shape[0], 256))
 
 
 def _dit_case(dim, heads, ffn, layers, H, W, seed):

@@ -16,7 +16,14 @@
   shift, scale and gate, which norm feeds which branch, the order of the
   three residuals) equals the closed forms of tests/block_probes.py exactly;
   every swap of two modulation chunks and every other residual order changes
-  at least one probe's output.
+  at least one probe's output;
+- the q/k RMSNorm wiring (causal_model.py:112-116, model.py:171-178): the
+  self-attention and cross-attention probes of tests/block_probes.py give
+  the oracle block exactly their closed forms (queries and keys sign * norm
+  weight, through the pinned RoPE, FP8 row codec, int8 linear and SDPA), the
+  oracle's text K/V equal tau_j * cnorm_k and a_j * c_v * tau_j bit for bit,
+  and each plausible mistake (a norm weight from the other norm, a norm
+  dropped) moves the closed form by more than 5 % relative L2.
 """
 
 import dataclasses
@@ -130,7 +137,7 @@ def test_rope_table_form_equals_scalar_float32():
             assert got[t, 0, 2 * i + 1] == bf16(np.float32(a * si) + np.float32(b * ci))
 
 
-PROBES = ("residuals", "ffn_mod", "attn_mod", "cross")
+PROBES = ("residuals", "ffn_mod", "attn_mod", "cross", "self_qk", "cross_q")
 
 
 def _run_probe(params, pr, e=None):
@@ -144,6 +151,8 @@ def _run_probe(params, pr, e=None):
 def test_block_wiring_equals_closed_form(kind):
     pr = bp.build(kind)
     assert torch.equal(_run_probe(pr["params"], pr), pr["expected"])
+    if kind in ("self_qk", "cross_q"):
+        return  # these probe the q/k norms (test_qk_norm_mistakes_move_the_closed_form)
     # another gate chunk or another residual order is visible in this probe
     for alt in bp.alternatives(pr):
         assert not torch.equal(alt, pr["expected"])
@@ -162,3 +171,25 @@ def test_every_swap_of_two_modulation_chunks_is_caught():
             if not torch.equal(_run_probe(p, pr, e=pr["e"][:, perm]), pr["expected"]):
                 caught.add((i, j))
     assert caught == set(itertools.combinations(range(6), 2))
+
+
+@pytest.mark.parametrize("kind", ["self_qk", "cross_q"])
+def test_qk_norm_mistakes_move_the_closed_form(kind):
+    pr = bp.build(kind)
+    want = pr["expected"].double()
+    alts = bp.qk_alternatives(pr)
+    assert len(alts) >= 4
+    for name, alt in alts.items():
+        rel = ((alt.double() - want).norm() / want.norm()).item()
+        assert rel > 5e-2, f"{kind}: '{name}' is within {rel:.2e} of the true wiring"
+
+
+def test_text_kv_equals_closed_form():
+    pr = bp.build("cross_q")
+    p, text = pr["params"], pr["text"]
+    k, v = ob.text_kv(p, text, bp.HEADS)
+    ck, cv = bp.text_kv_closed_form(p, text)
+    assert torch.equal(k, ck) and torch.equal(v, cv)
+    # the text K normalized with the query's weight, or not normalized, is another tensor
+    assert not torch.equal(k, bp.text_kv_closed_form(p, text, k_weight=p.cnorm_q)[0])
+    assert not torch.equal(k, bp.text_kv_closed_form(p, text, k_norm=False)[0])

@@ -11,15 +11,25 @@
 - flow -> x0: sigma = 0 returns xt, exact cases of xt - sigma * flow, and the
   float64 -> bf16 conversion goes through float32 as torch's does;
 - sigma at the warped DMD timesteps is the closed form 5s / (1 + 4s) of the
-  shifted schedule (1, 15/16, 5/6, 5/8), and the product's lookup equals it.
+  shifted schedule (1, 15/16, 5/6, 5/8), and the product's lookup equals it;
+- the activations of the time and text embeddings (causal_model.py:519-525,
+  840-855): with one-hot weights (tests/embed_probes.py) the time embedding
+  is bf16(silu(.)) of chosen sinusoid columns and the projection
+  bf16(silu(.)) of chosen e columns, the text embedding bf16(gelu_tanh(.)) of
+  chosen context columns plus the second bias (the bias alone on the padding
+  rows), each within one bf16 ulp of its float64 definition; a dropped SiLU,
+  a dropped GELU or a SiLU in the GELU's place moves most elements further.
 """
 
 import dataclasses
 import math
 
+import pytest
+
 import torch
 import torch.nn.functional as F
 
+import embed_probes as ep
 from oracle import dit as od
 from oracle import schedule as osch
 from waveforcing_amd.dit import random_dit_params
@@ -121,3 +131,27 @@ def test_sigma_at_warped_steps_closed_form_and_product_lookup():
         assert sched.sigma_x0(t) == s
     # between two table entries the nearer one wins (the first on a tie)
     assert od.sigma_x0(sig, ts, float(ts[10]) + 1e-3) == float(sig[10].double())
+
+
+@pytest.mark.parametrize("t", [1000.0, 937.5, 625.0, 3.0])
+def test_time_embedding_activations_closed_form(t):
+    p, picks = ep.time_probe(random_dit_params(64, seed=9))
+    e, e0 = od.time_embed(p, torch.full((3,), t, dtype=torch.float64))
+    want_e, want_e0 = ep.time_closed_form(t, 3, picks)
+    assert ep.within_one_ulp(e, want_e) and ep.within_one_ulp(e0, want_e0)
+    for name, (ae, ae0) in ep.time_alternatives(t, 3, picks).items():
+        far = max(ep.far_fraction(ae, want_e), ep.far_fraction(ae0, want_e0))
+        assert far > 0.3, f"{name}: only {far:.2f} of the elements move"
+
+
+def test_text_embedding_activation_and_padding_closed_form():
+    p, ctx, picks = ep.text_probe(random_dit_params(64, seed=10))
+    got = od.text_embed(p, ctx)
+    want = ep.text_closed_form(ctx, p.text2_b, picks)
+    assert got.shape == (512, 64)
+    assert ep.within_one_ulp(got, want)
+    # the rows that pad the context to 512 read back the second bias exactly
+    assert torch.equal(got[ctx.shape[0]:], p.text2_b.expand(512 - ctx.shape[0], 64))
+    for name, alt in ep.text_alternatives(ctx, p.text2_b, picks).items():
+        far = ep.far_fraction(alt[:ctx.shape[0]], want[:ctx.shape[0]])
+        assert far > 0.3, f"{name}: only {far:.2f} of the context rows' elements move"
