@@ -132,3 +132,34 @@ def test_thirty_layer_workload_properties():
             if layer in check:
                 c, s = okv.quantize_rows(x)
                 assert torch.equal(xo.cpu().to(torch.bfloat16), okv.dequantize_rows(c, s))
+
+
+def test_thirty_layer_single_launch_bit_exact():
+    """The launch the headline times: one pack of all 30 layers' K and V (140 400 tokens) into 90 pages
+    of a 180-page pool at the seeded page table, then one gather-dequant of the same 90 pages.  Codes and
+    scales on every one of the 90 pages, and both bf16 outputs, equal the oracle's bit for bit; the other
+    90 pages of the pool stay untouched."""
+    L, T, H, page = 30, 4680, 12, 1560
+    ppl = T // page
+    n_pages = L * ppl
+    P = 2 * n_pages
+    n = L * T
+    ids = inputs.page_table(n_pages, P, seed=7)
+    print(f"[case] 30 layers, {n} tokens, {n_pages} of {P} pages, one launch each way", flush=True)
+    k_all = torch.cat([inputs.kv_layer(layer)[0] for layer in range(L)])
+    v_all = torch.cat([inputs.kv_layer(layer)[1] for layer in range(L)])
+    pool = Fp8PagePool(P, H, 128, page, DEV)
+    table = pool.page_table(ids)
+    kd, vd = k_all.to(DEV), v_all.to(DEV)
+    pool.pack(kd, vd, table)
+    ko, vo = pool.unpack(table, n)
+    del kd, vd
+    unused = sorted(set(range(P)) - set(ids))
+    for x, xo, codes_pool, scales_pool in ((k_all, ko, pool.k_codes, pool.k_scales),
+                                          (v_all, vo, pool.v_codes, pool.v_scales)):
+        c, s = okv.quantize_rows(x)
+        assert torch.equal(codes_pool[ids].cpu(), c.view(n_pages, page, H, 128))
+        assert torch.equal(scales_pool[ids].cpu(), s.view(n_pages, page, H).transpose(1, 2))
+        assert int(codes_pool[unused].abs().sum()) == 0 and int(scales_pool[unused].abs().sum()) == 0
+        assert torch.equal(xo.cpu(), okv.dequantize_rows(c, s))
+        del c, s
