@@ -17,6 +17,11 @@ each tick runs the store rank's pass and the active denoise ranks' passes.
   max |diff| <= 5e-2 * max |x|), since every input x is fresh and only the
   context carries differences between the two sides.
 * A failing layer returns every slot of the tick and promotes nothing.
+* 14B composition: a 40-layer 14B stack's pass (each block's last gated
+  residual fused into the next block's first LayerNorm) equals 40 plain
+  single-block forward calls over the same contexts bit for bit, on a
+  denoise pass over two stored chunks; and a 3-layer 14B-width stack equals
+  the CPU oracle chained over its layers within the block bar.
 """
 
 import pytest
@@ -30,6 +35,8 @@ from waveforcing_amd import rope
 from waveforcing_amd.block import QuantizedWanBlock, random_block_params
 from waveforcing_amd.kv import Fp8PagePool
 from waveforcing_amd.stack import QuantizedWanStack
+
+H14, W14 = 30, 52        # a 4680-token chunk of 1560-token frames
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -221,3 +228,68 @@ def test_wavefront_refuses_mixed_or_misordered_passes():
     with pytest.raises(ValueError, match="denoise passes"):
         st.run_wavefront([(x, e, st.exchange.store_pass())], HT, WD)
     st.exchange.abort_tick()
+
+
+def _x14(seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((3 * H14 * W14, 5120), generator=g).to(torch.bfloat16)
+    e = (torch.randn((3, 6, 5120), generator=g) * 0.1).to(torch.bfloat16)
+    return x, e
+
+
+def test_14b_forty_layer_pass_equals_single_block_calls():
+    st = QuantizedWanStack.random("14b", seed=500, device=DEV, rf_step=4)
+    assert len(st.blocks) == 40
+    st.set_text(torch.randn((512, 5120), generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).to(DEV))
+    xch = st.exchange
+    for c in range(2):
+        x, e = _x14(600 + c)
+        st.forward_chunk(x.to(DEV), e.to(DEV), c, H14, W14, store=True)
+    x, e = _x14(610)
+    x, e = x.to(DEV), e.to(DEV)
+    plan = ex.TickPlan(2, [0], False, 2 * NPB, NPB)
+    xch.begin_tick(plan)
+    try:
+        p = xch.denoise_pass(0)
+        fused = x.clone()
+        st.run_pass(fused, e, p, H14, W14)
+        single = x.clone()
+        cos, sin = rope.cos_sin(NPB, H14, W14, p.chunk * NPB, 128, device=DEV)
+        n_ctx = set()
+        for L, blk in enumerate(st.blocks):
+            pool, ctx, own, n = xch.layer_context(L, p, H14, W14)
+            n_ctx.add(n)
+            blk.forward(single, e, cos, sin, pool, ctx, own, n, st.text_kv[L])
+        torch.cuda.synchronize()
+    finally:
+        xch.abort_tick()
+    print(f"context {sorted(n_ctx)} keys per layer; equal {(fused == single).double().mean().item():.6f}")
+    assert n_ctx == {3 * 4680}     # anchor + working chunk + self
+    assert torch.equal(fused, single)
+
+
+def test_14b_three_layer_stack_matches_oracle_chain():
+    dim, heads, ffn, layers = 5120, 40, 13824, 3
+    params = [random_block_params(dim, ffn, seed=520 + i) for i in range(layers)]
+    text = (torch.randn((512, dim), generator=torch.Generator().manual_seed(9))).to(torch.bfloat16)
+    blocks = [QuantizedWanBlock(q, heads, DEV) for q in params]
+    st = QuantizedWanStack(blocks, ex.PagedExchange(layers, heads, H14 * W14, NPB, 21, rf_step=4, device=DEV))
+    st.set_text(text.to(DEV))
+    x, e = _x14(620)
+    out = st.forward_chunk(x.to(DEV).clone(), e.to(DEV), 0, H14, W14).cpu().double()
+    del st, blocks
+    torch.cuda.empty_cache()
+    page = H14 * W14
+    ref = x
+    for L, q in enumerate(params):
+        pk, pv = okv.new_pool(NPB, page, heads, 128), okv.new_pool(NPB, page, heads, 128)
+        tk, tv = ob.text_kv(q, text, heads)
+        ref = ob.block_forward(q, ref, e, (NPB, H14, W14), 0, pk, pv, [0, 1, 2], [0, 1, 2], NPB * page, page,
+                               tk, tv, heads)
+        print(f"oracle layer {L} done", flush=True)
+    ref = ref.double()
+    rel = ((out - ref).norm() / ref.norm()).item()
+    mx = (out - ref).abs().max().item()
+    print(f"3-layer 14B stack vs oracle chain: rel L2 {rel:.3e}, max abs {mx:.3e}, max|x| {ref.abs().max().item():.2f}")
+    assert rel <= 1e-2
+    assert mx <= 5e-2 * ref.abs().max().item()
