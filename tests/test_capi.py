@@ -76,3 +76,20 @@ def test_row_kernels_refuse_launches_beyond_2_to_32_threads():
     with pytest.raises(RuntimeError, match="too large"):
         _lib.call("wf_ln_modulate_quant", 16, 1 << 24, 1536, 1536, 1e-6, None, None, None, None, 0, 4680, 32, 1536,
                   None, None, None)
+
+
+def test_index_kernels_refuse_launches_beyond_2_to_32_threads():
+    # one thread per item: 2^32 items or more, and sizes whose product overflows int64, are refused
+    with pytest.raises(RuntimeError, match="below 2\\^32"):
+        _lib.call("wf_patchify_bf16", 16, 1 << 20, 16, 3, 60, 104, 32, None)
+    with pytest.raises(RuntimeError, match="below 2\\^32"):
+        _lib.call("wf_patchify_bf16", 16, 1 << 40, 1 << 30, 1 << 30, 1 << 30, 1 << 30, 32, None)
+    with pytest.raises(RuntimeError, match="below 2\\^32"):
+        _lib.call("wf_unpatchify_flow_x0_bf16", 16, 32, 1 << 20, 16, 3, 60, 104, 0.5, 48, None)
+
+
+def test_gemm_sizes_that_overflow_int64_are_refused():
+    with pytest.raises(RuntimeError, match="2 GiB"):
+        _lib.call("wf_gemm_i8", 16, 32, 1 << 62, 16, 1 << 62, 48, 64, None, 80, 16, None, 0, None)
+    with pytest.raises(RuntimeError, match="2 GiB"):
+        _lib.call("wf_w8a8_linear", 16, 1 << 40, 1 << 40, 1 << 40, 32, 48, None, 16, 80, 16, 0, 96, 112, None)

@@ -213,3 +213,38 @@ def test_reset_starts_a_new_stream_with_the_same_contexts():
     x.reset()
     assert all(not c for c in x.clean) and all(len(f) == x.n_slots for f in x._free)
     assert stream() == first
+
+
+def test_anchor_rotation_follows_the_pass_grid(monkeypatch):
+    """The anchor pages are re-rotated when a pass has another (height, width) of the same token count and
+    the same rope start: the rotation in place is keyed by (start, height, width), not by the start alone."""
+    x = ex.PagedExchange(n_layers=1, n_heads=1, tokens_per_frame=16, frames_per_chunk=3, max_attn_frames=21,
+                         rf_step=1, device="cpu")
+    calls = []
+    monkeypatch.setattr(x.pool, "pack", lambda *a, **k: calls.append(k["rope"][0].clone()))
+    x.begin_tick_at(1, num_chunks=4)                       # the store pass of chunk 0: it becomes the anchor
+    x.context_slots(0, x.store_pass())
+    assert x.anchor_ku_out(0) is not None
+    x.end_tick()
+    x.begin_tick_at(2, num_chunks=4)
+    p = x.denoise_pass(0)
+    x.prepare_pass(p, 4, 4)
+    x.prepare_pass(p, 4, 4)                                 # memo: no second rotation
+    x.prepare_pass(p, 2, 8)                                 # another grid, same start and token count
+    x.prepare_pass(p, 4, 4)
+    x.abort_tick()
+    assert len(calls) == 3
+    assert not torch.equal(calls[0], calls[1]) and torch.equal(calls[0], calls[2])
+
+
+def test_table_cache_is_only_cleared_between_ticks(monkeypatch):
+    monkeypatch.setattr(ex, "TABLE_CACHE_MAX", 4)
+    x = ex.PagedExchange(n_layers=1, n_heads=1, tokens_per_frame=16, rf_step=1, device="cpu")
+    x.begin_tick_at(1, num_chunks=3)
+    tabs = [x.table(0, [s]) for s in range(x.n_slots)]
+    assert len(x._tables) == x.n_slots > 4              # inside a tick nothing is dropped
+    assert all(x.table(0, [s]) is t for s, t in enumerate(tabs))
+    x.abort_tick()
+    x.begin_tick_at(1, num_chunks=3)
+    assert not x._tables
+    x.abort_tick()

@@ -480,11 +480,11 @@ extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int
   WF_REQUIRE(n_kv == 0 || (k_codes && v_codes && k_scales && v_scales && page_table), WF_E_INVALID,
              "%s: null KV pool or page table", fn);
   WF_REQUIRE(page_tokens >= wf::BKV, WF_E_SHAPE, "%s: page_tokens=%d must be >= %d", fn, page_tokens, wf::BKV);
+  WF_REQUIRE(n_kv < (1ll << 31) && lq < (1ll << 31) && n_table < (1ll << 31), WF_E_SHAPE, "%s: size too large", fn);
   WF_REQUIRE(n_table * page_tokens >= n_kv, WF_E_SHAPE, "%s: page table covers %lld keys < n_kv=%lld", fn,
              (long long)(n_table * page_tokens), (long long)n_kv);
-  WF_REQUIRE(pool_pages * page_tokens * n_heads * head_dim < (1ll << 31) - 16, WF_E_SHAPE,
+  WF_REQUIRE(wf::product_below({pool_pages, page_tokens, n_heads, head_dim}, (1ll << 31) - 16), WF_E_SHAPE,
              "%s: a code pool of 2 GiB or more is not supported", fn);
-  WF_REQUIRE(n_kv < (1ll << 31) && lq < (1ll << 31) && n_table < (1ll << 31), WF_E_SHAPE, "%s: size too large", fn);
   WF_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15u) == 0 && (ldq % 8) == 0 &&
                  (reinterpret_cast<uintptr_t>(out) & 7u) == 0 && (ldo % 4) == 0,
              WF_E_ALIGN, "%s: q must be 16-byte aligned (ldq %% 8 == 0), out 8-byte aligned (ldo %% 4 == 0)", fn);
@@ -524,7 +524,8 @@ extern "C" int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads, in
   WF_REQUIRE(ldq >= hd && ldo >= hd && ldkv >= hd, WF_E_INVALID, "%s: row strides smaller than n_heads*head_dim", fn);
   if (lq == 0) return WF_OK;
   WF_REQUIRE(q && out && (n_kv == 0 || (k && v)), WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE(n_kv * ldkv * 2 < (1ll << 31) - 16 && lq < (1ll << 31), WF_E_SHAPE, "%s: K/V of 2 GiB or more", fn);
+  WF_REQUIRE(wf::product_below({n_kv, ldkv, 2}, (1ll << 31) - 16) && lq < (1ll << 31), WF_E_SHAPE,
+             "%s: K/V of 2 GiB or more", fn);
   WF_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15u) == 0 && ldq % 8 == 0 && (reinterpret_cast<uintptr_t>(k) & 15u) == 0 &&
                  (reinterpret_cast<uintptr_t>(v) & 15u) == 0 && ldkv % 8 == 0 &&
                  (reinterpret_cast<uintptr_t>(out) & 7u) == 0 && ldo % 4 == 0,

@@ -251,8 +251,10 @@ int wf_patchify_bf16(const void* x, int64_t b, int32_t c, int32_t f, int32_t h, 
   WF_REQUIRE(x && out, WF_E_INVALID, "%s: null pointer", fn);
   WF_REQUIRE((reinterpret_cast<uintptr_t>(x) & 3u) == 0 && (reinterpret_cast<uintptr_t>(out) & 7u) == 0, WF_E_ALIGN,
              "%s: x must be 4-byte and out 8-byte aligned", fn);
+  // one thread per item: a launch holds fewer than 2^32 threads
+  WF_REQUIRE(wf::product_below({b, f, h / 2, w / 2, c}, (1ll << 32) - 256), WF_E_SHAPE,
+             "%s: b*f*(h/2)*(w/2)*c must stay below 2^32 - 256", fn);
   const int64_t items = b * static_cast<int64_t>(f) * (h / 2) * (w / 2) * c;
-  WF_REQUIRE(items < (1ll << 40), WF_E_SHAPE, "%s: too large", fn);
   hipLaunchKernelGGL(wf::patchify_kernel, dim3(static_cast<uint32_t>((items + 255) / 256)), dim3(256), 0,
                      wf::as_stream(stream), static_cast<const uint16_t*>(x), b, c, f, h, w,
                      static_cast<uint16_t*>(out));
@@ -269,8 +271,10 @@ int wf_unpatchify_flow_x0_bf16(const void* head, const void* xt, int64_t b, int3
   WF_REQUIRE((reinterpret_cast<uintptr_t>(xt) & 3u) == 0 && (reinterpret_cast<uintptr_t>(x0) & 3u) == 0 &&
                  (reinterpret_cast<uintptr_t>(head) & 1u) == 0,
              WF_E_ALIGN, "%s: xt and x0 must be 4-byte aligned", fn);
+  // one thread per item: a launch holds fewer than 2^32 threads
+  WF_REQUIRE(wf::product_below({b, f, c, h, w / 2}, (1ll << 32) - 256), WF_E_SHAPE,
+             "%s: b*f*c*h*(w/2) must stay below 2^32 - 256", fn);
   const int64_t items = b * static_cast<int64_t>(f) * c * h * (w / 2);
-  WF_REQUIRE(items < (1ll << 40), WF_E_SHAPE, "%s: too large", fn);
   hipLaunchKernelGGL(wf::unpatchify_x0_kernel, dim3(static_cast<uint32_t>((items + 255) / 256)), dim3(256), 0,
                      wf::as_stream(stream), static_cast<const uint16_t*>(head), static_cast<const uint16_t*>(xt), b, c,
                      f, h, w, sigma, static_cast<uint16_t*>(x0));

@@ -526,7 +526,9 @@ extern "C" int wf_gemm_i8(const int8_t* a, const int8_t* w, int64_t m, int64_t n
              (long long)m, (long long)n, (long long)k, (long long)ldy);
   if (m == 0 || n == 0) return WF_OK;
   WF_REQUIRE(a && w && sx && sw && y, WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE((m + 256) * k < (1ll << 31) - 16 && (n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE,
+  WF_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && wf::product_below({m + 256, k}, (1ll << 31) - 16) &&
+                 wf::product_below({n + 256, k}, (1ll << 31) - 16),
+             WF_E_SHAPE,
              "%s: operands of 2 GiB or more are not supported", fn);
   WF_REQUIRE(k % 16 == 0 && k > 0, WF_E_SHAPE, "%s: k=%lld must be a positive multiple of 16", fn, (long long)k);
   WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);
@@ -547,7 +549,9 @@ extern "C" int wf_w8a8_linear(const void* x, int64_t m, int64_t k, int64_t ldx, 
              (long long)ldx, (long long)ldy);
   if (m == 0 || n == 0) return WF_OK;
   WF_REQUIRE(x && qw && sw && y && ws_q && ws_sx, WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE((m + 256) * k < (1ll << 31) - 16 && (n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE,
+  WF_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && wf::product_below({m + 256, k}, (1ll << 31) - 16) &&
+                 wf::product_below({n + 256, k}, (1ll << 31) - 16),
+             WF_E_SHAPE,
              "%s: operands of 2 GiB or more are not supported", fn);
   WF_REQUIRE(k % 16 == 0 && ldx % 8 == 0, WF_E_SHAPE, "%s: k %% 16 and ldx %% 8 must be 0", fn);
   WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);
@@ -571,7 +575,9 @@ extern "C" int wf_gemm_fp8_pertensor(const uint8_t* a, const uint8_t* w, int64_t
              (long long)m, (long long)n, (long long)k, (long long)ldy);
   if (m == 0 || n == 0) return WF_OK;
   WF_REQUIRE(a && w && a_scale && w_scale && y, WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE((m + 256) * k < (1ll << 31) - 16 && (n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE,
+  WF_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && wf::product_below({m + 256, k}, (1ll << 31) - 16) &&
+                 wf::product_below({n + 256, k}, (1ll << 31) - 16),
+             WF_E_SHAPE,
              "%s: operands of 2 GiB or more are not supported", fn);
   WF_REQUIRE(k % 16 == 0 && k > 0, WF_E_SHAPE, "%s: k=%lld must be a positive multiple of 16", fn, (long long)k);
   WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);
@@ -591,7 +597,9 @@ extern "C" int wf_fp8_linear_pertensor(const void* x, int64_t m, int64_t k, int6
   if (m == 0 || n == 0) return WF_OK;
   WF_REQUIRE(x && w_codes && w_scale && y && ws_codes && ws_scale && ws_partials, WF_E_INVALID, "%s: null pointer",
              fn);
-  WF_REQUIRE((m + 256) * k < (1ll << 31) - 16 && (n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE,
+  WF_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && wf::product_below({m + 256, k}, (1ll << 31) - 16) &&
+                 wf::product_below({n + 256, k}, (1ll << 31) - 16),
+             WF_E_SHAPE,
              "%s: operands of 2 GiB or more are not supported", fn);
   WF_REQUIRE(k % 16 == 0 && ldx % 8 == 0, WF_E_SHAPE, "%s: k %% 16 and ldx %% 8 must be 0", fn);
   WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);

@@ -438,8 +438,8 @@ int check_pool_args(const char* fn, int64_t n_tokens, int32_t n_heads, int32_t h
              "%s: negative or zero size (n_tokens=%lld n_heads=%d page_tokens=%d n_table=%lld pool_pages=%lld)", fn,
              (long long)n_tokens, n_heads, page_tokens, (long long)n_table, (long long)pool_pages);
   WF_REQUIRE(head_dim == kHeadDim, WF_E_SHAPE, "%s: head_dim=%d unsupported (must be 128)", fn, head_dim);
-  WF_REQUIRE(n_tokens * n_heads < (1ll << 31), WF_E_SHAPE, "%s: n_tokens*n_heads=%lld exceeds 2^31", fn,
-             (long long)(n_tokens * n_heads));
+  WF_REQUIRE(wf::product_below({n_tokens, n_heads}, 1ll << 31), WF_E_SHAPE,
+             "%s: n_tokens=%lld x n_heads=%d reaches 2^31", fn, (long long)n_tokens, n_heads);
   WF_REQUIRE(pool_pages < (1ll << 31) && n_table < (1ll << 31), WF_E_SHAPE, "%s: pool or table too large", fn);
   WF_REQUIRE(n_table * page_tokens >= n_tokens, WF_E_SHAPE,
              "%s: page table covers %lld tokens < n_tokens=%lld", fn, (long long)(n_table * page_tokens),

@@ -69,11 +69,12 @@ extern "C" int wf_w8a8_linear_static(const void* x, int64_t m, int64_t k, int64_
              "%s: bad sizes m=%lld n=%lld k=%lld ldx=%lld ldy=%lld", fn, (long long)m, (long long)n, (long long)k,
              (long long)ldx, (long long)ldy);
   if (m == 0 || n == 0) return WF_OK;
-  WF_REQUIRE(m <= kScratchRows && m * k <= kScratchCodeBytes, WF_E_SHAPE,
+  WF_REQUIRE(m <= kScratchRows && wf::product_below({m, k}, kScratchCodeBytes + 1), WF_E_SHAPE,
              "%s: m=%lld x k=%lld exceeds the static workspace (m <= %lld, m*k <= %lld bytes)", fn, (long long)m,
              (long long)k, (long long)kScratchRows, (long long)kScratchCodeBytes);
   WF_REQUIRE(x && qw && sw && y, WF_E_INVALID, "%s: null pointer", fn);
-  WF_REQUIRE((n + 256) * k < (1ll << 31) - 16, WF_E_SHAPE, "%s: weights of 2 GiB or more are not supported", fn);
+  WF_REQUIRE(n < (1ll << 31) && wf::product_below({n + 256, k}, (1ll << 31) - 16), WF_E_SHAPE,
+             "%s: weights of 2 GiB or more are not supported", fn);
   WF_REQUIRE(k % 16 == 0 && ldx % 8 == 0, WF_E_SHAPE, "%s: k %% 16 and ldx %% 8 must be 0", fn);
   WF_REQUIRE(n % 4 == 0 && ldy % 4 == 0, WF_E_SHAPE, "%s: n and ldy must be multiples of 4", fn);
   WF_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(qw) & 15u) == 0 &&

@@ -7,6 +7,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <initializer_list>
 
 #include "../../include/wf_api.h"
 
@@ -27,6 +28,21 @@ int check_launch(const char* what);
   } while (0)
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// True when the product of the non-negative factors is below ``limit`` (> 0), decided without forming a
+// product that could overflow int64: size checks of the entry points must not rely on wrapped arithmetic.
+inline bool product_below(std::initializer_list<int64_t> factors, int64_t limit) {
+  for (int64_t f : factors) {
+    if (f < 0) return false;
+    if (f == 0) return true;
+  }
+  int64_t p = 1;
+  for (int64_t f : factors) {
+    if (p > (limit - 1) / f) return false;
+    p *= f;
+  }
+  return p < limit;
+}
 
 // ------------------------------------------------------------------- bf16
 // bf16 -> fp32 is exact: the bf16 bits are the high half of the fp32 bits.

@@ -56,6 +56,7 @@ from . import rope
 from .kv import Fp8PagePool, PagedKV, PageTable
 
 MAX_CLEAN = 8  # anchor + the last 7 clean chunks (common.py:110-114)
+TABLE_CACHE_MAX = 4096  # cached page tables, cleared between ticks once reached
 
 
 def working_chunks(max_attn_frames: int, query_frames: int, frames_per_chunk: int) -> int:
@@ -161,7 +162,7 @@ class PagedExchange:
         # the anchor chunk's normalized, un-rotated K of every layer [Ln, T, H, D] (allocated with the first
         # store pass), and the anchor re-RoPE start its pages currently hold
         self.anchor_ku: torch.Tensor | None = None
-        self._anchor_rot: int | None = None
+        self._anchor_rot: tuple | None = None    # (rope_start, height, width) of the anchor pages' rotation
         self._plan: TickPlan | None = None
         self._store: Pass | None = None
         self._live: dict[int, int] = {}                                   # layer -> slot of the stored chunk
@@ -181,8 +182,6 @@ class PagedExchange:
         key = (layer, tuple(slots))
         t = self._tables.get(key)
         if t is None:
-            if len(self._tables) >= 4096:  # slot tuples recur as the ring turns; bound the cache anyway
-                self._tables.clear()
             t = self.pools[layer].page_table([p for s in slots for p in self.slot_pages(s)])
             self._tables[key] = t
         return t
@@ -246,7 +245,7 @@ class PagedExchange:
         if any(len(c) != len(self.clean[0]) for c in self.clean):
             raise RuntimeError("[paged] the layers' clean lists differ in length")
         start = anchor_rope_start(p.csf, len(self._working(0, p.qf)), self.npb)
-        if self._anchor_rot == start:
+        if self._anchor_rot == (start, height, width):
             return
         if self.npb * height * width != self.T:
             raise ValueError(f"grid {self.npb}x{height}x{width} does not hold the chunk's {self.T} tokens")
@@ -260,7 +259,7 @@ class PagedExchange:
             self._tables[key] = table
         self.pool.pack(self.anchor_ku.view(self.n_layers * self.T, self.n_heads, self.head_dim), None, table,
                        rope=(cos, sin), tiled=True)
-        self._anchor_rot = start
+        self._anchor_rot = (start, height, width)
 
     # ----------------------------------------------------------------- ticks
     def begin_tick(self, plan: TickPlan) -> TickPlan:
@@ -268,6 +267,10 @@ class PagedExchange:
             raise RuntimeError("[paged] the previous tick has not ended (end_tick / abort_tick)")
         if plan.act_ranks and (min(plan.act_ranks) < 0 or max(plan.act_ranks) >= self.rf_step):
             raise ValueError(f"[paged] active ranks {plan.act_ranks} outside 0..{self.rf_step - 1}")
+        # slot tuples recur as the ring turns, but the cache is bounded anyway; it is only cleared between ticks,
+        # where no kernel of this exchange's passes is still queued behind a stream the caller has not joined
+        if len(self._tables) >= TABLE_CACHE_MAX:
+            self._tables.clear()
         self._plan = plan
         return plan
 

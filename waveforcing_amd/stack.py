@@ -142,6 +142,10 @@ class QuantizedWanStack:
         evs = self._events
         while len(evs) < n:
             evs.append([torch.cuda.Event() for _ in self.blocks])
+        # every page table the passes read is built here, on the current stream, before the streams fork (in the
+        # loop's order, so each rank's in-flight slot is taken after the ranks above it): the caching allocator
+        # then ties them to the current stream, which waits for every side stream before it goes on
+        ctxs = [[ex.layer_context(L, p, height, width) for p in passes] for L in range(len(self.blocks))]
         cur = torch.cuda.current_stream(dev)
         streams = self.side_streams(n)
         try:
@@ -157,7 +161,7 @@ class QuantizedWanStack:
                         if i > 0:
                             st.wait_event(evs[i - 1][L])
                         x, pending, cos, sin, es_all = state[i]
-                        pool, ctx, own, n_ctx = ex.layer_context(L, p, height, width)
+                        pool, ctx, own, n_ctx = ctxs[L][i]
                         x, pending = blk.forward(x, e, cos, sin, pool, ctx, own, n_ctx, self.text_kv[L],
                                                  es=es_all[L], pending=pending, defer_residual=True, ws=wss[i])
                         state[i][0], state[i][1] = x, pending
