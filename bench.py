@@ -131,6 +131,19 @@ def bench_kv(steps: int, warmup: int, dev: str, which=("pack", "unpack", "pack_l
     return out
 
 
+def bench_kv_pertensor(steps: int, warmup: int, dev: str):
+    """The reference's per-tensor FP8 KV mode on one 1.3B layer: K/V [2, 4680, 12, 128] bf16 quantized with one
+    scale (amax pass + quantize) and dequantized to fp32, as ``_all_gather_fp8`` does on one rank."""
+    from waveforcing_amd.kv import pack_pertensor, unpack_pertensor
+
+    k, v = inputs.kv_layer(0)
+    kv = torch.stack([k, v]).to(dev)
+    ms = _timed(lambda: unpack_pertensor(*pack_pertensor(kv)), steps, warmup)
+    elems = kv.numel()
+    moved = elems * 2 * 2 + elems * 1 + elems * 1 + elems * 4   # amax read, quant read + write, dequant read + write
+    return {"us_round_trip": ms * 1e3, "bytes": moved, "gbs": moved / (ms * 1e-3) / 1e9}
+
+
 def bench_gemm(steps: int, warmup: int, dev: str):
     """W8A8 linear at the Wan-1.3B shape: the int8 GEMM alone, quant + GEMM, and the
     reference's per-tensor e4m3 GEMM alone and with its activation quantization."""
@@ -189,8 +202,9 @@ def bench_block_linears(steps: int, warmup: int, dev: str):
     return {"ms": ms, "ops": ops, "tops": ops / (ms * 1e-3) / 1e12}
 
 
-def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8):
-    """Paged FP8 attention: Q [4680, 12, 128] over `chunks` chunks (4680 keys each) of FP8 pages."""
+def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8, quantized_qk: bool = False):
+    """Paged FP8 attention: Q [4680, 12, 128] over `chunks` chunks (4680 keys each) of FP8 pages (with
+    ``quantized_qk``, the quantized-QK form: e4m3 queries against the K codes on the fp8 matrix cores)."""
     from waveforcing_amd.backend import attn_paged_fp8
     from waveforcing_amd.kv import PagedKV
 
@@ -207,15 +221,17 @@ def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8):
     q = torch.randn((TOKENS, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
     ctx = PagedKV(pool, table, n_kv)
     out = torch.empty_like(q)
-    ms = _timed(lambda: attn_paged_fp8(q, ctx, out=out), steps, warmup)
+    ms = _timed(lambda: attn_paged_fp8(q, ctx, out=out, quantized_qk=quantized_qk), steps, warmup)
     flops = 4.0 * TOKENS * n_kv * H * HEAD_DIM
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops, "keys": n_kv}
 
 
-def bench_block(scale: str, steps: int, warmup: int, dev: str):
+def bench_block(scale: str, steps: int, warmup: int, dev: str, quantized_qk: bool = False):
     """One quantized DiT block over one 3-frame chunk (4680 tokens, 30x52 latent grid) with 7 prior
-    chunks of FP8 paged context (37440 keys incl. its own) and a 512-token text context."""
+    chunks of FP8 paged context (37440 keys incl. its own) and a 512-token text context (with
+    ``quantized_qk``, the self-attention through the hip_fp8_qk backend)."""
     from waveforcing_amd import rope
+    from waveforcing_amd.backend import _WAVE_STATE, enable_hip_fp8, enable_hip_fp8_qk
     from waveforcing_amd.block import PRESETS, QuantizedWanBlock, random_block_params
 
     cfg = PRESETS[scale]
@@ -243,7 +259,13 @@ def bench_block(scale: str, steps: int, warmup: int, dev: str):
         x.copy_(x0)
         blk.forward(x, e, cos, sin, pool, ctx, own, (prior + 1) * T, tkv)
 
-    ms = _timed(step, steps, warmup)
+    saved = dict(_WAVE_STATE)
+    try:
+        (enable_hip_fp8_qk if quantized_qk else enable_hip_fp8)()
+        ms = _timed(step, steps, warmup)
+    finally:
+        _WAVE_STATE.clear()
+        _WAVE_STATE.update(saved)
     return {"ms": ms, "tokens": T, "context_keys": (prior + 1) * T}
 
 
@@ -602,7 +624,8 @@ def main() -> None:
                     help="minimum untimed warm-up of the KV workloads (profiler runs use 0)")
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
-                                       "tick_1p3b", "generate_1p3b", "copy"],
+                                       "tick_1p3b", "generate_1p3b", "copy", "attention_qk8", "block_1p3b_qk8",
+                                       "kv_pertensor"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -623,6 +646,9 @@ def main() -> None:
               "stack_1p3b": bench_stack, "stack_14b": lambda s, w, d: bench_stack(s, w, d, "14b"),
               "dit_1p3b": bench_dit, "tick_1p3b": lambda s, w, d: bench_stack(s, w, d, ticks_only=True),
               "generate_1p3b": bench_generate,
+              "attention_qk8": lambda s, w, d: bench_attention(s, w, d, quantized_qk=True),
+              "block_1p3b_qk8": lambda s, w, d: bench_block("1.3b", s, w, d, quantized_qk=True),
+              "kv_pertensor": bench_kv_pertensor,
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
@@ -631,7 +657,10 @@ def main() -> None:
     lin = bench_block_linears(max(5, args.steps // 5), 2, dev)
     at_sweep = {c: bench_attention(max(5, args.steps // 5), 2, dev, chunks=c) for c in (1, 2, 4, 8)}
     at = at_sweep[8]
+    at_qk = bench_attention(max(5, args.steps // 5), 2, dev, quantized_qk=True)
+    kvt = bench_kv_pertensor(max(5, args.steps // 5), 2, dev)
     b13 = bench_block("1.3b", max(5, args.steps // 5), 2, dev)
+    b13q = bench_block("1.3b", max(5, args.steps // 5), 2, dev, quantized_qk=True)
     b14 = bench_block("14b", max(3, args.steps // 10), 1, dev)
     xch = bench_exchange(max(5, args.steps // 5), 2, dev)
     stk = bench_stack(max(3, args.steps // 10), 1, dev)
@@ -701,6 +730,15 @@ def main() -> None:
             "attn_paged_fp8_roofline": {"bound": "mfma", "achieved": round(at["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
                                         "unit": "TFLOP/s", "frac": round(at["tflops"] / BF16_PEAK_TFLOPS, 4)},
             "attn_shape": "Q[4680,12,128] bf16 over 37440 keys (8 chunks) of FP8 e4m3fn pages, bf16 MFMA",
+            "attn_paged_fp8_qk8_ms": round(at_qk["ms"], 4),
+            "attn_paged_fp8_qk8_tflops": round(at_qk["tflops"], 1),
+            "attn_qk8_note": "the quantized-QK backend (hip_fp8_qk, the SageAttention counterpart): per-query e4m3 "
+                             "Q against the pages' K codes on the fp8 matrix cores, exact V; same workload",
+            "dit_block_1p3b_qk8_ms_per_chunk": round(b13q["ms"], 4),
+            "fp8_kv_pertensor_layer_us": round(kvt["us_round_trip"], 2),
+            "fp8_kv_pertensor_gbs": round(kvt["gbs"], 1),
+            "fp8_kv_pertensor_note": "the reference's per-tensor FP8 KV mode (_all_gather_fp8) on one layer's "
+                                     "K/V [2,4680,12,128]: amax + quantize (two launches) + fp32 dequant",
             "attn_paged_fp8_context_sweep": {f"{c}_chunks": {"keys": r["keys"], "ms": round(r["ms"], 4),
                                                               "tflops": round(r["tflops"], 1)}
                                              for c, r in at_sweep.items()},

@@ -274,6 +274,23 @@ int wf_fp8_linear_pertensor(const void* x, int64_t m, int64_t k, int64_t ldx,
                             uint8_t* ws_codes, float* ws_scale,
                             float* ws_partials, void* stream);
 
+/* ------------------------------------------------ FP8 KV, per tensor
+ *
+ * The reference's per-tensor FP8 KV exchange (_all_gather_fp8,
+ * wave_rt/denoiser/exchange/common.py:143-164): one scale per [2, T, H, D]
+ * K/V tensor.  The quantization is wf_fp8_quant_pertensor(kv viewed as
+ * [2 T H][D], WF_FP8_TENSOR_ACT): the scale is computed in bf16 arithmetic
+ * and the quotient rounded to bf16 before the e4m3 cast, as the reference's
+ * bf16 tensor divided by a 0-dim fp32 scale is (common.py:145-150).
+ */
+
+/* out[i] = fp32(e4m3(codes[i])) * (*scale) for i < n (exact in fp32), the
+ * reference's dequant codes.view(e4m3).to(bf16) * scale with a 1-element
+ * fp32 scale, whose result is fp32 (common.py:161-164).  scale points to
+ * one device fp32.  n % 16 == 0; codes and out 16-byte aligned. */
+int wf_fp8_dequant_pertensor_f32(const uint8_t* codes, const float* scale,
+                                 int64_t n, float* out, void* stream);
+
 /* ------------------------------------------------------------- attention */
 
 /* Attention of bf16 queries q [lq][n_heads][128] (token stride ldq
@@ -294,6 +311,23 @@ int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads,
                       int32_t page_tokens, const int32_t* page_table,
                       int64_t n_table, int64_t n_kv, float softmax_scale,
                       void* out, int64_t ldo, void* stream);
+
+/* The quantized-QK form of wf_attn_paged_fp8, same arguments: the
+ * counterpart of the reference's SageAttention backend (enable_sage /
+ * sageattn, wave_rt/runtime/backend.py:57-62,144-146), which quantizes Q and
+ * K before QK^T.  Each query row (per head) is quantized to e4m3 with its
+ * own scale s_q = amax|q| / 448; scores are sum_d code_q * code_k from the
+ * fp8 matrix cores (fp32 accumulation) times s_k * s_q; V and the softmax are
+ * exact as in wf_attn_paged_fp8.  Approximate by design (e4m3 queries carry
+ * 3 mantissa bits). */
+int wf_attn_paged_fp8_qk8(const void* q, int64_t lq, int32_t n_heads,
+                          int32_t head_dim, int64_t ldq,
+                          const uint8_t* k_codes, const uint8_t* v_codes,
+                          const float* k_scales, const float* v_scales,
+                          int64_t pool_pages, int32_t page_tokens,
+                          const int32_t* page_table, int64_t n_table,
+                          int64_t n_kv, float softmax_scale, void* out,
+                          int64_t ldo, void* stream);
 
 /* Attention of q [lq][n_heads][128] over dense bf16 K, V [n_kv][n_heads][128]
  * (token stride ldkv elements), same math and output as wf_attn_paged_fp8

@@ -43,3 +43,35 @@ def paged_fp8(q, k_pool, v_pool, table: Sequence[int], n_kv: int, page_tokens: i
     k = okv.unpack(table, n_kv, page_tokens, *k_pool)
     v = okv.unpack(table, n_kv, page_tokens, *v_pool)
     return sdpa(q, k, v, scale)
+
+
+def quantize_q_rows(q: torch.Tensor):
+    """e4m3 quantization of each query row (per head): s_q = amax|q| / 448 in fp32 (1 for an all-zero row) and
+    codes e4m3(clamp(q * (448 / amax), +-448)), where 448 / amax is the correctly rounded fp32 quotient (taken
+    through float64: torch's CPU scalar / tensor goes through the reciprocal and can land one ulp off, which
+    moves codes that sit on an e4m3 rounding tie).  q [Lq, H, D] bf16 -> (fp32 decoded codes [Lq, H, D],
+    s_q [Lq, H])."""
+    qf = q.float()
+    amax = qf.abs().amax(dim=-1)
+    inv = torch.where(amax > 0, (448.0 / amax.double()).float(), torch.zeros_like(amax))
+    s_q = torch.where(amax > 0, amax * (1.0 / 448.0), torch.ones_like(amax))
+    codes = (qf * inv[..., None]).clamp(-448.0, 448.0).to(okv.FP8).float()
+    return codes, s_q
+
+
+def paged_fp8_qk8(q, k_pool, v_pool, table: Sequence[int], n_kv: int, page_tokens: int, scale=None) -> torch.Tensor:
+    """The quantized-QK form of :func:`paged_fp8` (the counterpart of the reference's SageAttention backend,
+    wave_rt/runtime/backend.py:57-62,144-146, which quantizes Q and K before QK^T): scores
+    (sum_d code_q code_k) * s_q * s_k * scale over the e4m3 K codes of the pages and the per-row e4m3 queries of
+    :func:`quantize_q_rows`, softmax in float64, V the pages' bf16 dequantization.  -> fp32 [Lq, H, D]."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    kc, ks = okv.gather(table, n_kv, page_tokens, *k_pool)
+    v = okv.unpack(table, n_kv, page_tokens, *v_pool)
+    qc, sq = quantize_q_rows(q)
+    kcf = kc.view(okv.FP8).float().double()                       # [Lk, H, D]
+    out = []
+    for h in range(q.shape[1]):
+        s = (qc[:, h].double() @ kcf[:, h].T) * sq[:, h, None].double() * ks[:, h][None, :].double() * scale
+        out.append(torch.softmax(s, dim=-1) @ v[:, h].double())
+    return torch.stack(out, dim=1).float()

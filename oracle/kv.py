@@ -75,3 +75,20 @@ def unpack(table: Sequence[int], n_tokens: int, page_tokens: int, codes_pool, sc
     """Gather + dequantize to bf16 [T, H, D]."""
     codes, scales = gather(table, n_tokens, page_tokens, codes_pool, scales_pool)
     return dequantize_rows(codes, scales)
+
+
+# ------------------------------------------------------------ per tensor
+def quantize_tensor(kv: torch.Tensor):
+    """The reference's per-tensor FP8 KV quantization, wave_rt/denoiser/exchange/common.py:145-150, in its
+    own torch dtypes: the bf16 amax / 448 stays bf16, the clamp floor is bf16(1e-8), the scale is then cast to
+    fp32 (0-dim); bf16 kv divided by that 0-dim fp32 scale stays bf16 (the quotient is rounded to bf16) and is
+    cast to e4m3fn.  kv bf16 [...] -> (codes uint8 [...], scale fp32 [1])."""
+    assert kv.dtype == torch.bfloat16
+    scale = (kv.abs().amax() / E4M3_MAX).clamp(min=1e-8).to(torch.float32)
+    codes = (kv / scale).to(FP8).view(torch.uint8)
+    return codes, scale.reshape(1)
+
+
+def dequantize_tensor(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """common.py:161-164: ``codes.view(e4m3).to(bf16) * scale`` with the 1-element fp32 scale -> fp32."""
+    return codes.view(FP8).to(torch.bfloat16) * scale

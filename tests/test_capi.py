@@ -93,3 +93,12 @@ def test_gemm_sizes_that_overflow_int64_are_refused():
         _lib.call("wf_gemm_i8", 16, 32, 1 << 62, 16, 1 << 62, 48, 64, None, 80, 16, None, 0, None)
     with pytest.raises(RuntimeError, match="2 GiB"):
         _lib.call("wf_w8a8_linear", 16, 1 << 40, 1 << 40, 1 << 40, 32, 48, None, 16, 80, 16, 0, 96, 112, None)
+
+
+def test_pertensor_dequant_and_qk8_argument_errors():
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        _lib.call("wf_fp8_dequant_pertensor_f32", 16, 32, 40, 48, None)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        _lib.call("wf_fp8_dequant_pertensor_f32", 17, 32, 64, 48, None)
+    with pytest.raises(RuntimeError, match="head_dim=64"):
+        _lib.call("wf_attn_paged_fp8_qk8", 16, 4, 2, 64, 128, 32, 48, 64, 80, 4, 64, 96, 1, 64, 0.1, 112, 128, None)

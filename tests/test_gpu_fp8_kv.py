@@ -163,3 +163,33 @@ def test_thirty_layer_single_launch_bit_exact():
         assert int(codes_pool[unused].abs().sum()) == 0 and int(scales_pool[unused].abs().sum()) == 0
         assert torch.equal(xo.cpu(), okv.dequantize_rows(c, s))
         del c, s
+
+
+@pytest.mark.parametrize("T,H,heavy", [(4680, 12, True), (4680, 40, False), (37, 3, True), (1, 1, False)])
+def test_pertensor_kv_bit_exact(T, H, heavy):
+    """The reference's per-tensor FP8 KV mode (common.py:143-164) on [2, T, H, 128]: codes, the fp32 scale
+    and the fp32 dequantization equal the oracle bit for bit; all_gather_fp8 on one GPU returns the same."""
+    from waveforcing_amd.kv import all_gather_fp8, pack_pertensor, unpack_pertensor
+
+    if heavy:
+        kv = torch.stack([inputs.heavy_tailed_kv(T, H, 128, seed=60), inputs.heavy_tailed_kv(T, H, 128, seed=61)])
+    else:
+        kv = torch.randn((2, T, H, 128), generator=torch.Generator().manual_seed(62)).to(torch.bfloat16)
+    print(f"[case] per-tensor KV [2, {T}, {H}, 128] heavy={heavy}", flush=True)
+    codes, scale = pack_pertensor(kv.to(DEV))
+    deq = unpack_pertensor(codes, scale)
+    oc, osc = okv.quantize_tensor(kv)
+    assert torch.equal(codes.cpu(), oc) and torch.equal(scale.cpu(), osc)
+    assert deq.dtype == torch.float32 and torch.equal(deq.cpu(), okv.dequantize_tensor(oc, osc))
+    gathered = all_gather_fp8(kv.to(DEV))
+    assert len(gathered) == 1 and torch.equal(gathered[0], deq)
+
+
+def test_pertensor_kv_zero_tensor_takes_the_scale_floor():
+    from waveforcing_amd.kv import pack_pertensor, unpack_pertensor
+
+    kv = torch.zeros((2, 64, 2, 128), dtype=torch.bfloat16, device=DEV)
+    codes, scale = pack_pertensor(kv)
+    oc, osc = okv.quantize_tensor(kv.cpu())
+    assert torch.equal(scale.cpu(), osc) and int(codes.abs().sum()) == 0
+    assert int(unpack_pertensor(codes, scale).abs().sum()) == 0

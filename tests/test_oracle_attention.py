@@ -5,6 +5,13 @@ identical keys give the mean of V; a zero scale gives the mean of V; key
 order does not matter; and a float64 numpy evaluation of the definition
 agrees on random data.  The paged path equals attention over the plain
 concatenation of the dequantized rows (paging changes layout only).
+
+The quantized-QK form (paged_fp8_qk8): queries whose rows are already e4m3
+values times a power of two (amax = 448 * 2^k) pass the quantization
+unchanged, so the form reduces to the exact paged attention; a single key
+returns its V row; all-zero queries give the mean of V; each query row's
+codes are within half an e4m3 step of q * 448 / amax; and on N(0, 1) data the
+form stays within the attention bar of the exact one while differing from it.
 """
 
 import math
@@ -64,3 +71,65 @@ def test_paged_equals_concatenated():
     cv, sv = okv.quantize_rows(v)
     want = oat.sdpa(q, okv.dequantize_rows(ck, sk), okv.dequantize_rows(cv, sv))
     assert torch.equal(got, want)
+
+
+def _pool_of(k, v, page):
+    n = k.shape[0]
+    pages = -(-n // page)
+    ids = list(range(pages))[::-1]
+    kp, vp = okv.new_pool(pages, page, k.shape[1], 128), okv.new_pool(pages, page, k.shape[1], 128)
+    okv.pack(k, ids, page, *kp)
+    okv.pack(v, ids, page, *vp)
+    return kp, vp, ids
+
+
+def _e4m3_rows(n, heads, seed, pow2):
+    """bf16 [n, heads, 128] rows of random e4m3 values whose amax is 448, times 2^pow2 (exact in bf16)."""
+    g = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, 256, (n, heads, 128), generator=g, dtype=torch.uint8)
+    vals = codes.view(okv.FP8).float()
+    vals = torch.where(torch.isnan(vals), torch.zeros_like(vals), vals)
+    vals[:, :, 0] = 448.0
+    return (vals * 2.0 ** pow2).to(torch.bfloat16)
+
+
+def test_qk8_reduces_to_exact_form_on_representable_queries():
+    # queries and keys whose rows are e4m3 values times a power of two: the query codes are the rows
+    # themselves and the K scale is a power of two, so code * s_k is also the exact form's bf16 K
+    q = _e4m3_rows(40, 2, 11, -9)
+    k, v = _e4m3_rows(150, 2, 12, -8), _rand((150, 2, 128), 13)
+    kp, vp, ids = _pool_of(k, v, 64)
+    qc, sq = oat.quantize_q_rows(q)
+    assert torch.equal(qc * sq[..., None], q.float())
+    got = oat.paged_fp8_qk8(q, kp, vp, ids, 150, 64)
+    want = oat.paged_fp8(q, kp, vp, ids, 150, 64)
+    assert (got - want).abs().max().item() < 1e-4
+
+
+def test_qk8_closed_forms_and_error_scale():
+    k, v = _rand((1, 3, 128), 14), _rand((1, 3, 128), 15)
+    q = _rand((5, 3, 128), 16)
+    kp, vp, ids = _pool_of(k, v, 64)
+    one = oat.paged_fp8_qk8(q, kp, vp, ids, 1, 64)
+    assert torch.equal(one, okv.unpack(ids, 1, 64, *vp).float().expand(5, 3, 128))
+    k, v = _rand((200, 3, 128), 17), _rand((200, 3, 128), 18)
+    kp, vp, ids = _pool_of(k, v, 64)
+    zero = oat.paged_fp8_qk8(torch.zeros((4, 3, 128), dtype=torch.bfloat16), kp, vp, ids, 200, 64)
+    mean = okv.unpack(ids, 200, 64, *vp).double().mean(0).float()
+    assert (zero - mean).abs().max().item() < 1e-6
+    # codes within half an e4m3 step (2^-4 relative) of q * 448 / amax
+    q = _rand((64, 3, 128), 19)
+    qc, sq = oat.quantize_q_rows(q)
+    ideal = q.float() / sq[..., None]
+    assert ((qc - ideal).abs() <= ideal.abs() * 2.0 ** -4 + 2.0 ** -10).all()
+    assert qc.abs().amax().item() == 448.0
+    # 448 / amax is the correctly rounded fp32 quotient: with amax 3 and an element 1.125 the quotient is
+    # RN32(448 / 3) * 1.125 = 168 exactly, an e4m3 tie between 160 and 176 that rounds to even (160);
+    # torch's 448.0 / tensor(3.0) is one ulp above and would give 176
+    tie = torch.zeros((1, 1, 128), dtype=torch.bfloat16)
+    tie[0, 0, 0], tie[0, 0, 1] = 3.0, 1.125
+    assert float(oat.quantize_q_rows(tie)[0][0, 0, 1]) == 160.0
+    got = oat.paged_fp8_qk8(q, kp, vp, ids, 200, 64)
+    exact = oat.paged_fp8(q, kp, vp, ids, 200, 64)
+    err = (got - exact).abs().max().item()
+    assert 0 < err < 2e-2

@@ -112,3 +112,59 @@ def test_golden_fixture():
     assert np.array_equal(vc.numpy(), g["v_codes"]) and np.array_equal(vs.numpy(), g["v_scales"])
     # the zero row takes the scale floor bf16(1e-8) and all-zero codes
     assert ks[table[0], 0, 0].item() == torch.tensor(1e-8).to(torch.bfloat16).float().item()
+
+
+# ---- per-tensor FP8 KV (common.py:143-164)
+def test_pertensor_codes_and_scale_equal_the_pinned_activation_quantizer():
+    from oracle import linear as olin
+    kv = inputs.heavy_tailed_kv(96, 3, 128, seed=21)
+    codes, scale = okv.quantize_tensor(kv)
+    want_codes, want_scale = olin.fp8_quant_act(kv.reshape(-1, 128))
+    assert torch.equal(codes.reshape(-1, 128), want_codes.view(torch.uint8))
+    assert scale.shape == (1,) and float(scale) == float(want_scale)
+
+
+def test_pertensor_dtypes_and_closed_forms():
+    # amax = 448 * 2^-3: the scale is exactly 2^-3, and the row max encodes to 448 (0x7e)
+    kv = torch.zeros((2, 4, 1, 128), dtype=torch.bfloat16)
+    kv[0, 1, 0, 5] = 56.0
+    kv[1, 2, 0, 7] = -1.5
+    codes, scale = okv.quantize_tensor(kv)
+    assert scale.dtype == torch.float32 and float(scale) == 0.125
+    assert int(codes[0, 1, 0, 5]) == 0x7E and int(codes[1, 2, 0, 7]) == 0xD4   # -12: sign, exponent 3 + 7, mantissa .100
+    deq = okv.dequantize_tensor(codes, scale)
+    assert deq.dtype == torch.float32                  # the reference's dequant is fp32 by promotion
+    assert float(deq[0, 1, 0, 5]) == 56.0 and float(deq[1, 2, 0, 7]) == -1.5
+    # the scale is amax / 448 rounded to bf16: amax 1 gives bf16(1/448), not the fp32 quotient
+    one = torch.zeros((1, 1, 1, 128), dtype=torch.bfloat16)
+    one[0, 0, 0, 0] = 1.0
+    s = float(okv.quantize_tensor(one)[1])
+    assert s == float(torch.tensor(1 / 448, dtype=torch.float32).to(torch.bfloat16)) and s != float(
+        torch.tensor(1.0 / 448.0, dtype=torch.float32))
+    # an all-zero tensor takes the bf16 floor of 1e-8 (bits 0x322c)
+    z, zs = okv.quantize_tensor(torch.zeros((1, 2, 1, 128), dtype=torch.bfloat16))
+    assert int(z.abs().sum()) == 0
+    assert torch.tensor([float(zs)]).to(torch.bfloat16).view(torch.int16).item() == 0x322C
+
+
+def test_pertensor_quotient_is_rounded_to_bf16_before_the_cast():
+    """x / s is rounded to bf16 first: pick x, s where the fp32 quotient and its bf16 rounding encode to
+    different e4m3 codes, and check the oracle gives the code of the bf16-rounded quotient."""
+    s = 0.125 * (1 + 2 ** -7)                               # a bf16 scale (amax = 448 * s)
+    found = 0
+    for m in range(128, 256):
+        x = torch.tensor([m * 2.0 ** -7 * 1.25], dtype=torch.float32).to(torch.bfloat16)
+        q32 = x.float() / torch.tensor(s)
+        qb = q32.to(torch.bfloat16).float()
+        c32 = int(q32.to(okv.FP8).view(torch.uint8))
+        cb = int(qb.to(okv.FP8).view(torch.uint8))
+        if c32 == cb:
+            continue
+        kv = torch.zeros((1, 1, 1, 128), dtype=torch.bfloat16)
+        kv[0, 0, 0, 0] = torch.tensor(448 * s).to(torch.bfloat16)
+        kv[0, 0, 0, 1] = x
+        codes, scale = okv.quantize_tensor(kv)
+        assert float(scale) == s
+        assert int(codes[0, 0, 0, 1]) == cb
+        found += 1
+    assert found > 0

@@ -83,6 +83,7 @@ SIGNATURES: dict[str, list] = {
         _i64, _c_void_p, _i64, _i32, _c_void_p,
     ],
     "wf_fp8_quant_pertensor": [_c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "wf_fp8_dequant_pertensor_f32": [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p],
     "wf_gemm_fp8_pertensor": [
         _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
     ],
@@ -91,6 +92,10 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _c_void_p, _c_void_p, _c_void_p,
     ],
     "wf_attn_paged_fp8": [
+        _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _i64, _i32, _c_void_p, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p,
+    ],
+    "wf_attn_paged_fp8_qk8": [
         _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _i64, _i32, _c_void_p, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p,
     ],

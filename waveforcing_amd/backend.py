@@ -10,7 +10,11 @@ attention kernel runs non-causally over it.
 The HIP backend, ``hip_fp8``, takes the context as a page descriptor
 (:class:`waveforcing_amd.kv.PagedKV`) that the paged FP8 exchange returns in
 place of the dense ``Kb[:active_len]`` views (paged.py:246-247), and runs
-``wf_attn_paged_fp8`` on it.
+``wf_attn_paged_fp8`` on it.  ``hip_fp8_qk`` is the quantized-QK counterpart
+of the reference's SageAttention backend (``enable_sage``, backend.py:57-62,
+144-146): the same call over the same pages through ``wf_attn_paged_fp8_qk8``,
+which quantizes each query to e4m3 and runs QK^T on the fp8 matrix cores
+against the pages' K codes, with V exact; approximate by design, like Sage.
 """
 
 from __future__ import annotations
@@ -24,7 +28,7 @@ import torch
 from . import _lib
 from .kv import PagedKV
 
-ATTENTION_BACKENDS = ("torch_sdpa", "fa_custom", "sa", "fa", "fa2", "hip_fp8")
+ATTENTION_BACKENDS = ("torch_sdpa", "fa_custom", "sa", "fa", "fa2", "hip_fp8", "hip_fp8_qk")
 
 _WAVE_STATE: dict = {
     "exchange_fn": None,
@@ -54,11 +58,14 @@ def prof_read() -> tuple:
 
 
 def attn_paged_fp8(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, causal: bool = False,
-                   softmax_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                   softmax_scale: float | None = None, out: torch.Tensor | None = None,
+                   quantized_qk: bool = False) -> torch.Tensor:
     """flash_attn_func-shaped call: q [1, Lq, H, D] (or [Lq, H, D]) bf16 over a paged FP8 context.
 
     ``k`` carries both pools; ``v`` is accepted for call compatibility and
-    must be ``k`` itself or None.  Returns bf16 with q's shape.
+    must be ``k`` itself or None.  Returns bf16 with q's shape.  With
+    ``quantized_qk`` the scores come from e4m3 queries against the K codes
+    on the fp8 matrix cores (wf_attn_paged_fp8_qk8).
     """
     if causal:
         raise ValueError("the wavefront attention is non-causal over the context (backend.py:141-148)")
@@ -80,7 +87,7 @@ def attn_paged_fp8(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, causal
     if o.dim() == 4:
         o = o[0]
     _lib.call(
-        "wf_attn_paged_fp8", q3.data_ptr(), Lq, H, D, q3.stride(0),
+        "wf_attn_paged_fp8_qk8" if quantized_qk else "wf_attn_paged_fp8", q3.data_ptr(), Lq, H, D, q3.stride(0),
         pool.k_codes.data_ptr(), pool.v_codes.data_ptr(), pool.k_scales.data_ptr(), pool.v_scales.data_ptr(),
         pool.pool_pages, pool.page_tokens, k.table.dev.data_ptr(), len(k.table), k.n_tokens,
         float(softmax_scale), o.data_ptr(), o.stride(0), _lib.stream_handle(q3.device),
@@ -114,16 +121,35 @@ def attn_dense_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_s
     return o
 
 
+def attn_paged_fp8_qk(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, causal: bool = False,
+                      softmax_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The quantized-QK form of :func:`attn_paged_fp8` (the ``fa_func`` of ``hip_fp8_qk``)."""
+    return attn_paged_fp8(q, k, v, causal, softmax_scale, out, quantized_qk=True)
+
+
 def enable_hip_fp8() -> None:
     """Use the gfx950 paged-FP8 attention on the wavefront path."""
     _WAVE_STATE["attn"] = "hip_fp8"
     _WAVE_STATE["fa_func"] = attn_paged_fp8
 
 
+def enable_hip_fp8_qk() -> None:
+    """Use the quantized-QK paged-FP8 attention on the wavefront path, as ``enable_sage`` selects
+    SageAttention (backend.py:57-62): e4m3 queries against the pages' K codes on the fp8 matrix cores."""
+    _WAVE_STATE["attn"] = "hip_fp8_qk"
+    _WAVE_STATE["fa_func"] = attn_paged_fp8_qk
+
+
+def paged_attention():
+    """The paged attention the blocks run: the quantized-QK form when ``hip_fp8_qk`` is selected, the exact
+    form otherwise."""
+    return attn_paged_fp8_qk if _WAVE_STATE["attn"] == "hip_fp8_qk" else attn_paged_fp8
+
+
 def attend(roped_query, ctx_k, ctx_v, sdpa: Callable | None = None):
     """Attention dispatch of the patched forward (backend.py:141-148)."""
     attn = _WAVE_STATE["attn"]
-    if attn == "hip_fp8":
+    if attn in ("hip_fp8", "hip_fp8_qk"):
         return _WAVE_STATE["fa_func"](roped_query, ctx_k, ctx_v, causal=False)
     if attn == "fa_custom":
         return _WAVE_STATE["fa_func"](roped_query, ctx_k, ctx_v, causal=False)

@@ -28,7 +28,7 @@ from dataclasses import dataclass, fields
 import torch
 
 from . import _lib, rope
-from .backend import attn_dense_bf16, attn_paged_fp8
+from .backend import attn_dense_bf16, paged_attention
 from .fp8 import _quant_rows_i8, gemm_i8
 from .kv import Fp8PagePool, PagedKV, PageTable
 
@@ -324,7 +324,7 @@ class QuantizedWanBlock:
         pool.pack_k_norm_rope(k, v, own_table, self.norm_k, EPS, (cos, sin), ku_out=unroped_k_out, q=q,
                               norm_q=self.norm_q)
         ctx = PagedKV(pool, context_table, n_context)
-        attn_paged_fp8(q.view(T, H, hd), ctx, out=ws["attn"].view(T, H, hd))
+        paged_attention()(q.view(T, H, hd), ctx, out=ws["attn"].view(T, H, hd))
         _linear_i8(ws["attn"], self.o, aq, as_, ws["y"])
 
         # gated residual + norm3 (affine) + quant -> q, RMSNorm, attention over text, o

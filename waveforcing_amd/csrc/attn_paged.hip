@@ -64,6 +64,8 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
 
 constexpr int D = 128;
 constexpr int BKV = 64;                 // keys per tile
@@ -77,6 +79,15 @@ constexpr int VP = D * 2 + 64;          // V row pitch (bytes) = 320: the 4 rows
 constexpr int K_TILE = BKV * KP;
 constexpr int V_TILE = BKV * VP;
 constexpr int STAGE = K_TILE + V_TILE;
+// The quantized-QK form keeps K as e4m3 codes in LDS: [key][d] rows of 128 codes at a 144-byte pitch (the 16-byte
+// fragment reads of 16 consecutive rows then start 36 dwords apart, on 16 distinct 4-bank groups), then V as
+// above, then the tile's 64 K scales.
+constexpr int KP8 = D + 16;
+constexpr int K8_TILE = BKV * KP8;
+constexpr int KS_BYTES = BKV * 4;
+constexpr int STAGE8 = K8_TILE + V_TILE + KS_BYTES;
+constexpr int OPITCH = D * 2 + 8;       // staged output row pitch (bytes)
+constexpr int OUT_STAGING = WAVES * 32 * OPITCH;
 constexpr int kBufferRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
 constexpr int kOutOfRange = 0x7ffffff0;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -148,9 +159,19 @@ __device__ inline float pair_sum(float v) {
   return a + b;
 }
 
-template <bool DENSE>
+// QK8: the quantized-QK form (the counterpart of the reference's SageAttention backend, backend.py:57-62,
+// 144-146).  Each query is quantized once to e4m3 with its own scale s_q = amax|q| / 448, the e4m3 K codes of the
+// pages are used as they are, and S^T = K_codes Q_codes^T runs on the fp8 matrix cores
+// (v_mfma_f32_32x32x64_f8f6f4); every score is then multiplied by its key's s_k, and s_q joins the softmax
+// scale in the exponent's FMA.  V and P stay exact as in the bf16 form.
+template <bool DENSE, bool QK8>
 __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  static_assert(!(DENSE && QK8), "the quantized-QK form reads FP8 pages");
+  constexpr int kStage = QK8 ? STAGE8 : STAGE;
+  constexpr int kVOff = QK8 ? K8_TILE : K_TILE;  // V rows within a stage
+  constexpr int kSOff = K8_TILE + V_TILE;        // K scales within a stage (QK8)
+  constexpr int kLds = 2 * kStage > OUT_STAGING ? 2 * kStage : OUT_STAGING;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -251,7 +272,15 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // The staged tile as bf16 [key][d] row pieces (registers only), and their
   // write into LDS stage `buf`.
   auto dequant_tile = [&](uint4* out) {
-    if constexpr (DENSE) {
+    if constexpr (QK8) {
+      // K codes as they are, the K scale alongside; V as in the bf16 form
+      out[0] = make_uint4(sk0[0], sk0[1], sk0[2], sk0[3]);
+      out[1] = make_uint4(__builtin_bit_cast(uint32_t, ssk), 0u, 0u, 0u);
+      const uint2 e = dequant4_bf16(sv0[0], ssv), f = dequant4_bf16(sv0[1], ssv);
+      const uint2 g = dequant4_bf16(sv0[2], ssv), i = dequant4_bf16(sv0[3], ssv);
+      out[2] = make_uint4(e.x, e.y, f.x, f.y);
+      out[3] = make_uint4(g.x, g.y, i.x, i.y);
+    } else if constexpr (DENSE) {
       out[0] = make_uint4(sk0[0], sk0[1], sk0[2], sk0[3]);
       out[1] = make_uint4(sk1[0], sk1[1], sk1[2], sk1[3]);
       out[2] = make_uint4(sv0[0], sv0[1], sv0[2], sv0[3]);
@@ -268,10 +297,15 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
     }
   };
   auto write_tile = [&](int buf, const uint4* v) {
-    uint4* dk = reinterpret_cast<uint4*>(lds + buf * STAGE + skey * KP + schunk * 32);
-    uint4* dv = reinterpret_cast<uint4*>(lds + buf * STAGE + K_TILE + skey * VP + schunk * 32);
-    dk[0] = v[0];
-    dk[1] = v[1];
+    uint4* dv = reinterpret_cast<uint4*>(lds + buf * kStage + kVOff + skey * VP + schunk * 32);
+    if constexpr (QK8) {
+      *reinterpret_cast<uint4*>(lds + buf * kStage + skey * KP8 + schunk * 16) = v[0];
+      if (schunk == 0) *reinterpret_cast<uint32_t*>(lds + buf * kStage + kSOff + skey * 4) = v[1].x;
+    } else {
+      uint4* dk = reinterpret_cast<uint4*>(lds + buf * kStage + skey * KP + schunk * 32);
+      dk[0] = v[0];
+      dk[1] = v[1];
+    }
     dv[0] = v[2];
     dv[1] = v[3];
   };
@@ -282,8 +316,49 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   };
 
   // ---- Q^T fragments for this wave's 32 queries (kept for the whole kernel)
-  v8bf qf[8];
-  {
+  v8bf qf[QK8 ? 1 : 8];
+  v8i qc[2];             // QK8: e4m3 codes of d = 64 m + 32 half + 0..31 (m = 0, 1)
+  float cq = p.qk_scale;  // the exponent's scale: softmax scale * log2(e), times s_q in the QK8 form
+  if constexpr (QK8) {
+    // lane (l32, half) holds d = 64 m + 32 half + 0..31 of query l32, the K positions its fp8 operand bytes
+    // stand for (the K fragments below use the same assignment)
+    const int q = q0 + wave * 32 + l32;
+    const bool ok = q < p.Lq;
+    const uint16_t* qp = p.q + static_cast<int64_t>(ok ? q : 0) * p.ldq + h * D + half * 32;
+    uint4 raw[8];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        raw[4 * m + j] = *reinterpret_cast<const uint4*>(qp + 64 * m + 8 * j);
+        if (!ok) raw[4 * m + j] = make_uint4(0, 0, 0, 0);
+      }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo_to_f32(w[e])), fabsf(bf16_hi_to_f32(w[e]))));
+    }
+    amax = pair_max(amax);
+    const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+    cq = (amax > 0.f ? amax * (1.0f / 448.0f) : 1.0f) * p.qk_scale;
+    auto code = [&](float v) { return fminf(fmaxf(v * inv, -448.0f), 448.0f); };
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      uint32_t c8[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 r = raw[4 * m + j];
+        c8[2 * j] = e4m3_pack4_hw(code(bf16_lo_to_f32(r.x)), code(bf16_hi_to_f32(r.x)), code(bf16_lo_to_f32(r.y)),
+                                  code(bf16_hi_to_f32(r.y)));
+        c8[2 * j + 1] = e4m3_pack4_hw(code(bf16_lo_to_f32(r.z)), code(bf16_hi_to_f32(r.z)),
+                                      code(bf16_lo_to_f32(r.w)), code(bf16_hi_to_f32(r.w)));
+      }
+      qc[m] = v8i{static_cast<int>(c8[0]), static_cast<int>(c8[1]), static_cast<int>(c8[2]), static_cast<int>(c8[3]),
+                  static_cast<int>(c8[4]), static_cast<int>(c8[5]), static_cast<int>(c8[6]), static_cast<int>(c8[7])};
+    }
+  } else {
     const int q = q0 + wave * 32 + l32;
     const bool ok = q < p.Lq;
     const uint16_t* qp = p.q + static_cast<int64_t>(ok ? q : 0) * p.ldq + h * D + half * 8;
@@ -303,13 +378,13 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // group G points at row 16t + 8r + 4 (G / 2) + s / 4, d = 32 db + 16 (G % 2)
   // + 4 (s % 4): lane i then holds d = 32 db + 16 (G % 2) + i and keys
   // 16t + 8r + 4 half + j, the key order of its P registers.
-  const int k_lane = l32 * KP + half * 16;
-  const int v_lane = K_TILE + (4 * half + ((lane & 15) >> 2)) * VP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
+  const int k_lane = QK8 ? l32 * KP8 + half * 32 : l32 * KP + half * 16;
+  const int v_lane = kVOff + (4 * half + ((lane & 15) >> 2)) * VP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
 
   v16f o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  const float c = p.qk_scale;
+  const float c = cq;
   float m_use = -INFINITY;  // maximum used in the exponents (raw score units)
   float m_thr = -INFINITY;  // rescale when a tile's maximum exceeds this
   float neg_mc = 0.f;       // -m_use * c
@@ -325,31 +400,66 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // the masking of keys past n_kv.
   auto body = [&](int it, auto LAST) {
     const int cur = it & 1;
-    const uint8_t* st = lds + cur * STAGE;
+    const uint8_t* st = lds + cur * kStage;
 
-    // K fragments of the tile, all in flight before the first MFMA.
-    v8bf kf[2][8];
+    uint4 nxt[4];
+    v16f s[2];
+    float4 skv[2][4];  // QK8: s_k of the lane's keys 32 b + 8 g + 4 half + 0..3
+    if constexpr (QK8) {
+      // K code fragments (32 bytes per MFMA: d = 64 m + 32 half + 0..31 of key 32 b + l32) and the lane's
+      // key scales (the same 16 per half-wave: broadcast reads), all in flight before the first MFMA
+      v8i kf8[2][2];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const uint8_t* a = st + k_lane + b * 32 * KP8 + 64 * m;
+          const v4i lo = *reinterpret_cast<const v4i*>(a);
+          const v4i hi = *reinterpret_cast<const v4i*>(a + 16);
+          kf8[b][m] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
 #pragma unroll
       for (int b = 0; b < 2; ++b)
-        kf[b][ks] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(st + k_lane + b * 32 * KP + ks * 32));
-    // S^T = K Q^T for 2 blocks of 32 keys, with the next tile's dequantization
-    // (registers only) between the MFMAs.
-    uint4 nxt[4];
-    dequant_tile(nxt);
-    v16f s[2];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) s[b] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        for (int g = 0; g < 4; ++g)
+          skv[b][g] = *reinterpret_cast<const float4*>(st + kSOff + 4 * (32 * b + 8 * g + 4 * half));
+      dequant_tile(nxt);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+      for (int b = 0; b < 2; ++b) s[b] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-      for (int b = 0; b < 2; ++b) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[b][ks], qf[ks], s[b], 0, 0, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the 16 K-fragment reads first
+      for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // then 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // and 4 VALU, alternating
+        for (int b = 0; b < 2; ++b)
+          s[b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf8[b][m], qc[m], s[b], 0, 0, 0, 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the 8 K-fragment and 8 scale reads first
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // then 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // and 8 VALU, alternating
+      }
+    } else {
+      // K fragments of the tile, all in flight before the first MFMA.
+      v8bf kf[2][8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          kf[b][ks] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(st + k_lane + b * 32 * KP + ks * 32));
+      // S^T = K Q^T for 2 blocks of 32 keys, with the next tile's dequantization
+      // (registers only) between the MFMAs.
+      dequant_tile(nxt);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) s[b] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[b][ks], qf[ks], s[b], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the 16 K-fragment reads first
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // then 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // and 4 VALU, alternating
+      }
     }
     // the next tile into the other stage (freed by the last barrier), the
     // loads of the one after, and this tile's V^T operands (in flight
@@ -367,6 +477,18 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
         vf[t][db] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
 
+    if constexpr (QK8) {
+      // each score times its key's scale
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          s[b][4 * g] *= skv[b][g].x;
+          s[b][4 * g + 1] *= skv[b][g].y;
+          s[b][4 * g + 2] *= skv[b][g].z;
+          s[b][4 * g + 3] *= skv[b][g].w;
+        }
+    }
     if constexpr (decltype(LAST)::value) {
       const int key_base = it * BKV;
 #pragma unroll
@@ -429,8 +551,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // tile's barrier has retired every read of the stages), then store 256-byte row segments.
   const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  constexpr int OPITCH = D * 2 + 8;  // staged row pitch (bytes)
-  static_assert(WAVES * 32 * OPITCH <= 2 * STAGE, "output staging fits the stages");
+  static_assert(OUT_STAGING <= kLds, "output staging fits the stages");
   uint8_t* ow = lds + wave * 32 * OPITCH;
 #pragma unroll
   for (int db = 0; db < 4; ++db) {
@@ -452,22 +573,21 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
 
 }  // namespace
 
-template <bool DENSE>
+template <bool DENSE, bool QK8>
 int launch_attn(const AttnArgs& p, int64_t lq, int n_heads, hipStream_t stream) {
   const int64_t items = (lq + BQ - 1) / BQ * n_heads;
   const dim3 grid(static_cast<uint32_t>((items + 7) / 8 * 8));
-  hipLaunchKernelGGL((attn_paged_fp8_kernel<DENSE>), grid, dim3(THREADS), 0, stream, p);
-  return check_launch(DENSE ? "wf_attn_dense_bf16" : "wf_attn_paged_fp8");
+  hipLaunchKernelGGL((attn_paged_fp8_kernel<DENSE, QK8>), grid, dim3(THREADS), 0, stream, p);
+  return check_launch(DENSE ? "wf_attn_dense_bf16" : QK8 ? "wf_attn_paged_fp8_qk8" : "wf_attn_paged_fp8");
 }
 
 }  // namespace wf
 
-extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int32_t head_dim, int64_t ldq,
-                                 const uint8_t* k_codes, const uint8_t* v_codes, const float* k_scales,
-                                 const float* v_scales, int64_t pool_pages, int32_t page_tokens,
-                                 const int32_t* page_table, int64_t n_table, int64_t n_kv, float softmax_scale,
-                                 void* out, int64_t ldo, void* stream) {
-  static const char* fn = "wf_attn_paged_fp8";
+namespace {
+int attn_paged_entry(const char* fn, bool qk8, const void* q, int64_t lq, int32_t n_heads, int32_t head_dim,
+                     int64_t ldq, const uint8_t* k_codes, const uint8_t* v_codes, const float* k_scales,
+                     const float* v_scales, int64_t pool_pages, int32_t page_tokens, const int32_t* page_table,
+                     int64_t n_table, int64_t n_kv, float softmax_scale, void* out, int64_t ldo, void* stream) {
   WF_REQUIRE(lq >= 0 && n_heads > 0 && n_kv >= 0 && page_tokens > 0 && n_table >= 0 && pool_pages >= 0,
              WF_E_INVALID, "%s: negative or zero size", fn);
   WF_REQUIRE(head_dim == wf::D, WF_E_SHAPE, "%s: head_dim=%d unsupported (must be 128)", fn, head_dim);
@@ -509,7 +629,29 @@ extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int
   p.pool_pages = static_cast<int>(pool_pages);
   p.page_div = wf::FastDiv(static_cast<uint32_t>(page_tokens));
   p.qk_scale = softmax_scale * wf::kLog2e;
-  return wf::launch_attn<false>(p, lq, n_heads, wf::as_stream(stream));
+  return qk8 ? wf::launch_attn<false, true>(p, lq, n_heads, wf::as_stream(stream))
+             : wf::launch_attn<false, false>(p, lq, n_heads, wf::as_stream(stream));
+}
+}  // namespace
+
+extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int32_t head_dim, int64_t ldq,
+                                 const uint8_t* k_codes, const uint8_t* v_codes, const float* k_scales,
+                                 const float* v_scales, int64_t pool_pages, int32_t page_tokens,
+                                 const int32_t* page_table, int64_t n_table, int64_t n_kv, float softmax_scale,
+                                 void* out, int64_t ldo, void* stream) {
+  return attn_paged_entry("wf_attn_paged_fp8", false, q, lq, n_heads, head_dim, ldq, k_codes, v_codes, k_scales,
+                          v_scales, pool_pages, page_tokens, page_table, n_table, n_kv, softmax_scale, out, ldo,
+                          stream);
+}
+
+extern "C" int wf_attn_paged_fp8_qk8(const void* q, int64_t lq, int32_t n_heads, int32_t head_dim, int64_t ldq,
+                                     const uint8_t* k_codes, const uint8_t* v_codes, const float* k_scales,
+                                     const float* v_scales, int64_t pool_pages, int32_t page_tokens,
+                                     const int32_t* page_table, int64_t n_table, int64_t n_kv, float softmax_scale,
+                                     void* out, int64_t ldo, void* stream) {
+  return attn_paged_entry("wf_attn_paged_fp8_qk8", true, q, lq, n_heads, head_dim, ldq, k_codes, v_codes, k_scales,
+                          v_scales, pool_pages, page_tokens, page_table, n_table, n_kv, softmax_scale, out, ldo,
+                          stream);
 }
 
 extern "C" int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads, int32_t head_dim, int64_t ldq,
@@ -544,5 +686,5 @@ extern "C" int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads, in
   p.page_tokens = 1;
   p.page_div = wf::FastDiv(1);
   p.qk_scale = softmax_scale * wf::kLog2e;
-  return wf::launch_attn<true>(p, lq, n_heads, wf::as_stream(stream));
+  return wf::launch_attn<true, false>(p, lq, n_heads, wf::as_stream(stream));
 }

@@ -100,6 +100,30 @@ __global__ __launch_bounds__(kThreads) void quant_tensor_kernel(Geometry g, cons
   }
 }
 
+// out[i] = fp32(code[i]) * s, 16 codes per thread per pass.  The product of a 4-bit e4m3 significand and an
+// 8-bit (bf16-derived) scale significand is exact in fp32: this is the reference's
+// `codes.view(e4m3).to(bf16) * scale` with a 1-element fp32 scale, whose result type is fp32
+// (wave_rt/denoiser/exchange/common.py:161-164).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kThreads) void dequant_tensor_f32_kernel(const u32x4* __restrict__ codes,
+                                                                      const float* __restrict__ scale, int64_t n16,
+                                                                      f32x4* __restrict__ out) {
+  const float s = scale[0];
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n16;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const u32x4 w = __builtin_nontemporal_load(codes + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float a, b, c, d;
+      e4m3_unpack4_hw(w[j], a, b, c, d);
+      const f32x4 v = {a * s, b * s, c * s, d * s};
+      __builtin_nontemporal_store(v, out + 4 * i + j);
+    }
+  }
+}
+
 }  // namespace
 
 int launch_fp8_quant_pertensor(const void* x, int64_t rows, int64_t k, int64_t ldx, int mode, uint8_t* codes,
@@ -133,4 +157,23 @@ extern "C" int wf_fp8_quant_pertensor(const void* x, int64_t rows, int64_t k, in
   WF_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(codes) & 7u) == 0,
              WF_E_ALIGN, "%s: x must be 16-byte and codes 8-byte aligned", fn);
   return wf::launch_fp8_quant_pertensor(x, rows, k, ldx, mode, codes, scale, ws_partials, wf::as_stream(stream));
+}
+
+extern "C" int wf_fp8_dequant_pertensor_f32(const uint8_t* codes, const float* scale, int64_t n, float* out,
+                                            void* stream) {
+  static const char* fn = "wf_fp8_dequant_pertensor_f32";
+  WF_REQUIRE(n >= 0, WF_E_INVALID, "%s: n=%lld is negative", fn, (long long)n);
+  if (n == 0) return WF_OK;
+  WF_REQUIRE(n % 16 == 0, WF_E_SHAPE, "%s: n=%lld must be a multiple of 16", fn, (long long)n);
+  WF_REQUIRE(n < (1ll << 40), WF_E_SHAPE, "%s: n=%lld too large", fn, (long long)n);
+  WF_REQUIRE(codes && scale && out, WF_E_INVALID, "%s: null pointer", fn);
+  WF_REQUIRE((reinterpret_cast<uintptr_t>(codes) & 15u) == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0 &&
+                 (reinterpret_cast<uintptr_t>(scale) & 3u) == 0,
+             WF_E_ALIGN, "%s: codes and out must be 16-byte aligned", fn);
+  const int64_t n16 = n / 16;
+  const int64_t blocks = (n16 + wf::kThreads - 1) / wf::kThreads;
+  const dim3 grid(static_cast<uint32_t>(blocks < 8192 ? blocks : 8192));
+  hipLaunchKernelGGL(wf::dequant_tensor_f32_kernel, grid, dim3(wf::kThreads), 0, wf::as_stream(stream),
+                     reinterpret_cast<const wf::u32x4*>(codes), scale, n16, reinterpret_cast<wf::f32x4*>(out));
+  return wf::check_launch(fn);
 }

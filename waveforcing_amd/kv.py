@@ -305,3 +305,46 @@ def fp8_decode(codes: torch.Tensor) -> torch.Tensor:
     _lib.call("wf_fp8_e4m3_decode_f32", codes.data_ptr(), out.data_ptr(), codes.numel(),
               _lib.stream_handle(codes.device))
     return out
+
+
+def pack_pertensor(kv: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The reference's per-tensor FP8 KV quantization (``_all_gather_fp8``,
+    wave_rt/denoiser/exchange/common.py:145-150): bf16 K/V [..., D] ->
+    (e4m3fn codes as uint8, same shape; fp32 scale [1]).  The scale is
+    ``(amax|kv| / 448).clamp(min=1e-8)`` in bf16 arithmetic, then fp32; the
+    quotient kv / scale is rounded to bf16 before the e4m3 cast."""
+    if kv.dtype != torch.bfloat16:
+        raise ValueError(f"pack_pertensor expects bf16 K/V, got {kv.dtype}")
+    if kv.numel() == 0 or kv.shape[-1] % 8:
+        raise ValueError(f"pack_pertensor needs a non-empty tensor whose last dim is a multiple of 8, got "
+                         f"{tuple(kv.shape)}")
+    kv = kv.contiguous()
+    D = kv.shape[-1]
+    codes = torch.empty(kv.shape, dtype=torch.uint8, device=kv.device)
+    scale = torch.empty((1,), dtype=torch.float32, device=kv.device)
+    partials = torch.empty((_lib.FP8_AMAX_PARTIALS,), dtype=torch.float32, device=kv.device)
+    _lib.call("wf_fp8_quant_pertensor", kv.data_ptr(), kv.numel() // D, D, D, _lib.FP8_TENSOR_ACT, codes.data_ptr(),
+              scale.data_ptr(), partials.data_ptr(), _lib.stream_handle(kv.device))
+    return codes, scale
+
+
+def unpack_pertensor(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """fp32 ``codes.view(e4m3).to(bf16) * scale`` (common.py:161-164; the 1-element fp32 scale makes the
+    result fp32)."""
+    if codes.dtype != torch.uint8 or scale.dtype != torch.float32 or scale.numel() != 1:
+        raise ValueError("unpack_pertensor takes uint8 codes and a 1-element fp32 scale")
+    codes = codes.contiguous()
+    out = torch.empty(codes.shape, dtype=torch.float32, device=codes.device)
+    _lib.call("wf_fp8_dequant_pertensor_f32", codes.data_ptr(), scale.data_ptr(), codes.numel(), out.data_ptr(),
+              _lib.stream_handle(codes.device))
+    return out
+
+
+def all_gather_fp8(mine: torch.Tensor, world: int = 1) -> list[torch.Tensor]:
+    """``_all_gather_fp8`` (common.py:143-164) on one GPU: quantize this rank's K/V [2, T, H, D] per tensor and
+    return the dequantized fp32 tensors of the ``world`` ranks, here all this rank's (a single-GPU gather of
+    one rank's codes and scale is the identity)."""
+    if world != 1:
+        raise ValueError("one GPU holds one rank: world must be 1 (the multi-GPU gather is not built)")
+    codes, scale = pack_pertensor(mine)
+    return [unpack_pertensor(codes, scale)]
