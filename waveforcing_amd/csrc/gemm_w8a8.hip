@@ -53,6 +53,13 @@
 //    persistent form (one workgroup per CU walking its tiles as one K-step
 //    pipeline, whose epilogue had no free LDS to stage in), the rounds are
 //    4-7 % faster on every multi-round Wan shape.
+//
+// Phase timing (built only with -DWF_GEMM_PHASES, never in the product library): the first and the
+// fifth wave of every workgroup (the two waves of SIMD 0) record the shader clock (s_memtime) at kernel
+// entry, after the prologue barrier, after the K loop's last barrier and after the epilogue's last
+// store, into a buffer registered with wf_gemm_set_phase_buffer: 8 stamps per workgroup,
+// [wave 0: 4][wave 4: 4].  waveforcing_amd/gemm_phases.py builds that variant and summarizes the
+// stamps (prologue, cycles per K step, epilogue).
 #include <type_traits>
 #include <utility>
 
@@ -153,7 +160,23 @@ struct GemmArgs {
   int M, N, K;
   int64_t ldy;
   int vec16;             // y and ldy allow 16-byte row stores
+  uint64_t* phases;      // phase-timing stamps (instrumented build only), or null
 };
+
+// Stamp `slot` of this workgroup's phase record (instrumented build only; a no-op otherwise).
+__device__ inline void phase_stamp(const GemmArgs& p, int wave, int lane, int slot) {
+#ifdef WF_GEMM_PHASES
+  if (p.phases != nullptr && (wave == 0 || wave == NW / 2)) {
+    const uint64_t t = __builtin_amdgcn_s_memtime();
+    if (lane == 0) p.phases[static_cast<int64_t>(blockIdx.x) * 8 + (wave == 0 ? 0 : 4) + slot] = t;
+  }
+#else
+  (void)p;
+  (void)wave;
+  (void)lane;
+  (void)slot;
+#endif
+}
 
 // The epilogue operands of the 256 columns from n0 into epi: sw by wave 0 (one 1 KB DMA), bias by wave 1
 // (two 256-byte DMAs).  Columns past N read as zero (N % 4 == 0, so no access straddles the end).
@@ -199,6 +222,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  phase_stamp(p, wave, lane, 0);
   const int wm = wave / WN;
   const int wn = wave % WN;
   const int l32 = lane & 31;
@@ -329,6 +353,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   }
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  phase_stamp(p, wave, lane, 1);
   // the bias as fp32 for the epilogue (published by the first K step's barrier)
   if constexpr (HAS_BIAS) {
     if (wave == 1) {
@@ -395,6 +420,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   wait_counts<0, 0>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  phase_stamp(p, wave, lane, 2);
   if (nk < 2) read_epi();
 
   // Each wave converts its 64 x 64 sub-tile as two 32-row slabs; a slab goes to the wave's own LDS area
@@ -456,7 +482,11 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
       }
     }
   }
+  phase_stamp(p, wave, lane, 3);
 }
+
+// The phase-stamp buffer of the instrumented build (null in the product library).
+uint64_t* g_phase_buffer = nullptr;
 
 GemmArgs make_args(const void* a, const void* w, int64_t M, int64_t N, int64_t K, const float* sx, const float* sw,
                    const void* bias, void* y, int64_t ldy, int32_t* acc_out) {
@@ -473,6 +503,7 @@ GemmArgs make_args(const void* a, const void* w, int64_t M, int64_t N, int64_t K
   p.K = static_cast<int>(K);
   p.ldy = ldy;
   p.vec16 = (ldy % 8 == 0) && ((reinterpret_cast<uintptr_t>(y) & 15u) == 0);
+  p.phases = g_phase_buffer;
   return p;
 }
 
@@ -612,3 +643,12 @@ extern "C" int wf_fp8_linear_pertensor(const void* x, int64_t m, int64_t k, int6
     return rc;
   return wf::launch_gemm_fp8_pertensor(ws_codes, w_codes, m, n, k, ws_scale, w_scale, bias, y, ldy, st);
 }
+
+#ifdef WF_GEMM_PHASES
+// Instrumented build only (not declared in wf_api.h): register a device buffer of 8 uint64 per workgroup
+// for the phase stamps of the following GEMM launches, or null to stop recording.
+extern "C" int wf_gemm_set_phase_buffer(uint64_t* stamps) {
+  wf::g_phase_buffer = stamps;
+  return WF_OK;
+}
+#endif
