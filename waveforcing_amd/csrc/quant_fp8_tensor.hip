@@ -22,6 +22,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kChunksPerThread = 4;  // 8-element chunks per thread per pass of the amax loop
+constexpr int kQuantBlocks = 2048;   // cap of the quantizing grid
 
 __device__ inline float block_max(float v, float* red) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -132,8 +133,10 @@ int launch_fp8_quant_pertensor(const void* x, int64_t rows, int64_t k, int64_t l
   const int64_t want = (g.total + kThreads * kChunksPerThread - 1) / (kThreads * kChunksPerThread);
   const int n_partials = static_cast<int>(want < WF_FP8_AMAX_PARTIALS ? (want > 0 ? want : 1) : WF_FP8_AMAX_PARTIALS);
   hipLaunchKernelGGL(amax_partials_kernel, dim3(n_partials), dim3(kThreads), 0, stream, g, partials);
+  // At most 2048 quantizing workgroups, each first reducing the (<= 1024) partials from L2: with one
+  // workgroup per 2048 elements the partials' reads added up to about the tensor's own size.
   const int64_t qblocks = (g.total + kThreads - 1) / kThreads;
-  const dim3 qgrid(static_cast<uint32_t>(qblocks < 4096 ? (qblocks > 0 ? qblocks : 1) : 4096));
+  const dim3 qgrid(static_cast<uint32_t>(qblocks < kQuantBlocks ? (qblocks > 0 ? qblocks : 1) : kQuantBlocks));
   if (mode == WF_FP8_TENSOR_ACT)
     hipLaunchKernelGGL((quant_tensor_kernel<true>), qgrid, dim3(kThreads), 0, stream, g, partials, n_partials, codes,
                        scale);
