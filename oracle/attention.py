@@ -64,14 +64,20 @@ def paged_fp8_qk8(q, k_pool, v_pool, table: Sequence[int], n_kv: int, page_token
     wave_rt/runtime/backend.py:57-62,144-146, which quantizes Q and K before QK^T): scores
     (sum_d code_q code_k) * s_q * s_k * scale over the e4m3 K codes of the pages and the per-row e4m3 queries of
     :func:`quantize_q_rows`, softmax in float64, V the pages' bf16 dequantization.  -> fp32 [Lq, H, D]."""
-    if scale is None:
-        scale = 1.0 / math.sqrt(q.shape[-1])
     kc, ks = okv.gather(table, n_kv, page_tokens, *k_pool)
     v = okv.unpack(table, n_kv, page_tokens, *v_pool)
+    return sdpa_qk8(q, kc, ks, v, scale)
+
+
+def sdpa_qk8(q, k_codes, k_scales, v, scale=None) -> torch.Tensor:
+    """The quantized-QK attention over dense operands: q [Lq, H, D] bf16, K as e4m3 codes [Lk, H, D] (uint8)
+    with scales [Lk, H], v [Lk, H, D] -> fp32 [Lq, H, D] (the body of :func:`paged_fp8_qk8`)."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
     qc, sq = quantize_q_rows(q)
-    kcf = kc.view(okv.FP8).float().double()                       # [Lk, H, D]
+    kcf = k_codes.view(okv.FP8).float().double()                  # [Lk, H, D]
     out = []
     for h in range(q.shape[1]):
-        s = (qc[:, h].double() @ kcf[:, h].T) * sq[:, h, None].double() * ks[:, h][None, :].double() * scale
+        s = (qc[:, h].double() @ kcf[:, h].T) * sq[:, h, None].double() * k_scales[:, h][None, :].double() * scale
         out.append(torch.softmax(s, dim=-1) @ v[:, h].double())
     return torch.stack(out, dim=1).float()

@@ -15,7 +15,8 @@ rotation at ``csf - wflen - npb``.  Checked for every (pass, layer):
 * the oracle's per-(token, head) quantize/dequantize of that context equals,
   bit for bit, the dequantized pages the closure hands to attention;
 * the attention output equals the oracle's fp32 SDPA over that context within
-  2e-2 max-abs;
+  2e-2 max-abs (with the ``hip_fp8_qk`` backend, the oracle's quantized-QK
+  attention over the context's codes, same bar);
 * ``prof_read()`` reports the context length as ``klen`` and positive
   exchange and attention times.
 
@@ -45,8 +46,9 @@ def _kv(t, rank, layer):
     return mk(), mk(), mk(), mk()          # q, roped K, un-rotated K, V
 
 
-def _model_context(clean, live, inflight, plan, rank, layer):
-    """Dequantized K, V of the list model's context for a pass (rank RF = store)."""
+def _model_context(clean, live, inflight, plan, rank, layer, raw=False):
+    """Dequantized K, V of the list model's context for a pass (rank RF = store); with ``raw`` the bf16 K and
+    V before their FP8 round trip."""
     if rank == RF:
         csf, qf = (plan.tick - RF) * NPB, NPB
     else:
@@ -66,14 +68,17 @@ def _model_context(clean, live, inflight, plan, rank, layer):
         chunks = ([live] if plan.store_active else []) + [inflight[n] for n in ex.inflight_order(rank, plan.act_ranks)]
     ks += [c["kr"][layer][0] for c in chunks]
     vs += [c["v"][layer][0] for c in chunks]
+    if raw:
+        return torch.cat(ks, 0), torch.cat(vs, 0)
     rt = lambda x: okv.dequantize_rows(*okv.quantize_rows(x))
     return rt(torch.cat(ks, 0)), rt(torch.cat(vs, 0))
 
 
-def test_wavefront_contexts_and_patched_attention_match_list_model():
+@pytest.mark.parametrize("attn", ["hip_fp8", "hip_fp8_qk"])
+def test_wavefront_contexts_and_patched_attention_match_list_model(attn):
     x = ex.PagedExchange(n_layers=LAYERS, n_heads=H, tokens_per_frame=HT * WD, frames_per_chunk=NPB,
                          max_attn_frames=WINDOW, rf_step=RF, device=DEV)
-    backend.enable_hip_fp8()
+    (backend.enable_hip_fp8 if attn == "hip_fp8" else backend.enable_hip_fp8_qk)()
     clean = []
     longest = 0
     try:
@@ -114,7 +119,12 @@ def test_wavefront_contexts_and_patched_attention_match_list_model():
                     assert ctx.shape == (1, wk.shape[0], H, 128) and klen == wk.shape[0]
                     assert torch.equal(k.cpu(), wk) and torch.equal(vv.cpu(), wv), f"tick {t} rank {rank} L{layer}"
                     assert attn_ms > 0 and exch_ms > 0
-                    ref = oat.sdpa(q[0], wk, wv)
+                    if attn == "hip_fp8":
+                        ref = oat.sdpa(q[0], wk, wv)
+                    else:
+                        kc, ksc = okv.quantize_rows(_model_context(clean, live, inflight, plan, rank, layer,
+                                                                   raw=True)[0])
+                        ref = oat.sdpa_qk8(q[0], kc, ksc, wv)
                     err = (out[0].cpu().float() - ref).abs().max().item()
                     assert out.shape == q.shape and err <= 2e-2, f"tick {t} rank {rank} L{layer}: {err:.3e}"
                     longest = max(longest, wk.shape[0])
