@@ -18,11 +18,16 @@
 //   s     = bf16_rne(amax / 448)         (bf16 arithmetic as in the reference)
 //   s     = max(s, bf16(1e-8))           (.clamp(min=1e-8)), then to fp32
 //   code  = e4m3_rne(min(|x| / s, 448)) with the sign of x
-// |x| / s is the correctly rounded fp32 quotient: q = |x| * r with
-// r = RN(1/s), then one residual step q += fma(-q, s, |x|) * r.  The
-// quotient of two 8-bit significands is either exact (and the residual step
-// returns it exactly) or at least 2^-14 (relative) away from every e4m3
-// rounding boundary, so the code equals that of the IEEE quotient.
+// amax / 448 is taken as amax * RN(1/448): rounded to bf16 it equals the
+// bf16 of the IEEE quotient for every bf16 amax (amax / 448 = (m / 7) 2^k
+// with an 8-bit m is either a short exact value or a repeating binary
+// fraction far from every bf16 rounding boundary; checked exhaustively).
+// |x| / s: q = |x| * r with r = v_rcp_f32(s) (within one ulp of 1/s), then
+// one residual step q += fma(-q, s, |x|) * r.  The quotient of two 8-bit
+// significands is either exact (and the residual step returns it exactly)
+// or at least 2^-14 (relative) away from every e4m3 rounding boundary, so
+// the code equals that of the IEEE quotient (checked over every pair of
+// significands, for both reciprocals next to 1/s).
 //
 // Two fused producers feed the same pages:
 // * kv_pack_kernel<..., ROPE = true> rotates K by a per-token RoPE table
@@ -95,7 +100,7 @@ __device__ inline bool locate(const PageGeom& g, uint32_t r, int64_t& code_row, 
   return true;
 }
 
-// Four e4m3 codes of bf16-exact values x[0..3] with scale s (r = RN(1/s)).
+// Four e4m3 codes of bf16-exact values x[0..3] with scale s (r within one ulp of 1/s).
 __device__ inline uint32_t quant4f(const float* x, float s, float r) {
   float q[4];
 #pragma unroll
@@ -144,8 +149,10 @@ __device__ inline float absmax8(const uint4& a, const uint4& b) {
   return m;
 }
 
+// bf16(amax / 448) as bf16(amax * RN(1/448)) (see above), floored at bf16(1e-8).
+constexpr float kInvE4M3Max = 1.0f / kE4M3Max;
 __device__ inline float scale_from_amax(float amax) {
-  const float s = bf16_bits_to_f32(f32_to_bf16_rne(__fdiv_rn(amax, kE4M3Max)));
+  const float s = bf16_bits_to_f32(static_cast<uint16_t>(pack_bf16x2_hw(amax * kInvE4M3Max, 0.f)));
   return fmaxf(s, bf16_bits_to_f32(kScaleFloorBf16Bits));
 }
 
@@ -210,7 +217,7 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(const uint4* __restrict__ 
   // every lane of the 8-lane group takes part in the reduction
   const float amax = group8_max(absmax8(a, b));
   const float s = scale_from_amax(amax);
-  const float rcp = __frcp_rn(s);
+  const float rcp = __builtin_amdgcn_rcpf(s);
   uint4 c;
   c.x = quant4(a.x, a.y, s, rcp);
   c.y = quant4(a.z, a.w, s, rcp);
@@ -266,7 +273,7 @@ __device__ inline void pack_head_chunk(const float* y, int ch, bool valid, bool 
   for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(y[i]));
   const float amax = rows::group16_max(m);
   const float s = scale_from_amax(amax);
-  const float r = __frcp_rn(s);
+  const float r = __builtin_amdgcn_rcpf(s);
   const uint2 c = make_uint2(quant4f(y, s, r), quant4f(y + 4, s, r));
   if (valid && placed) {
     const int h = ch >> 4;
