@@ -139,6 +139,38 @@ def test_single_key_returns_its_value_exactly():
     assert torch.equal(out, vrow.expand_as(out))
 
 
+@pytest.mark.parametrize("entry", ["wf_attn_paged_fp8", "wf_attn_paged_fp8_qk8"])
+def test_invalid_page_ids_read_as_zero_keys(entry):
+    """Table entries outside the pool (-1, or the pool size) read as zero codes and zero scales: their keys
+    score 0 and carry V = 0.  Pages of 200 tokens hold several tiles and tiles straddle page ends, so the
+    kernel moves its page bases within valid and invalid pages and recomputes them at every page start.
+    Such tables reach the kernel only through the C ABI (the Python page table refuses them)."""
+    Lq, H, page, P = 96, 3, 200, 6
+    n_kv = 4 * page + 77
+    k, v, q = _normal((n_kv, H, 128), 70), _normal((n_kv, H, 128), 71), _normal((Lq, H, 128), 72)
+    ids = [4, 0, 5, 2, 1]
+    pool = Fp8PagePool(P, H, 128, page, DEV)
+    pool.pack(k.to(DEV), v.to(DEV), pool.page_table(ids))
+    bad = list(ids)
+    bad[1], bad[3] = -1, P
+    table = torch.tensor(bad, dtype=torch.int32, device=DEV)
+    qd = q.to(DEV)
+    out = torch.empty((Lq, H, 128), dtype=torch.bfloat16, device=DEV)
+    _lib.call(entry, qd.data_ptr(), Lq, H, 128, qd.stride(0), pool.k_codes.data_ptr(), pool.v_codes.data_ptr(),
+              pool.k_scales.data_ptr(), pool.v_scales.data_ptr(), P, page, table.data_ptr(), len(bad), n_kv,
+              1.0 / math.sqrt(128), out.data_ptr(), out.stride(0), _lib.stream_handle(DEV))
+    kc, ks = okv.quantize_rows(k)
+    vz = okv.dequantize_rows(*okv.quantize_rows(v)).clone()
+    for lp in (1, 3):
+        rows = slice(lp * page, (lp + 1) * page)
+        kc[rows], ks[rows], vz[rows] = 0, 0.0, 0
+    kz = okv.dequantize_rows(kc, ks)
+    ref = oat.sdpa(q, kz, vz) if entry == "wf_attn_paged_fp8" else oat.sdpa_qk8(q, kc, ks, vz)
+    err = (out.cpu().float() - ref).abs().max().item()
+    print(f"{entry}: max abs err {err:.3e}")
+    assert err <= TOL, err
+
+
 def test_backend_dispatch_and_scale():
     q, pool, ctx, ids, kp, vp, _ = _setup(64, 2, 300, 128, 4, seed=30)
     saved = dict(_WAVE_STATE)

@@ -219,11 +219,67 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   u32x4 sk0, sv0, sk1, sv1;
   float ssk = 0.f, ssv = 0.f;
 
-  // Issue the loads of the tile starting at key t0.  A 64-key tile spans at
-  // most two pages (page_tokens >= 64, checked on the host); the page
-  // lookups are uniform across the workgroup.
-  auto load_tile = [&](int t0) {
+  // Page cursor of a tile (uniform across the workgroup): keys [0, split) of a tile starting at key t0 sit
+  // on the physical page of logical page lp from row r0 (split = page_tokens - r0), keys [split, 64) on
+  // the next logical page's from row 0 (a 64-key tile spans at most two pages: page_tokens >= 64,
+  // checked on the host).  cb0 / cb1 and sb0 / sb1 are the code and scale byte offsets a lane adds its
+  // key's row offset to (codes: skey * H * D + h * D + 16 schunk; scales: 4 skey), pushed beyond the
+  // buffer ranges (>= kOutOfRange > pool size, reading as zero) for an invalid page.  The bases are
+  // uint32: cb1 / sb1 wrap below zero when the next page is physical page 0 and a lane adds at least
+  // `split` rows back; an out-of-range base plus a row offset stays above every buffer range.
+  struct Cursor {
+    int r0;
+    uint32_t cb0, cb1, sb0, sb1;
+  };
+  // With the page lookups: the first tile and every tile that starts on a new page.  The lookups are
+  // awaited here (the empty asm uses them), never across the next tile's LDS reads: a page-table load
+  // in flight there turns the waits for its K-fragment reads into waits for everything (it counts in
+  // lgkmcnt with them and returns out of order).
+  auto cursor_at = [&](int t0) -> Cursor {
     if constexpr (DENSE) {
+      (void)t0;
+      return Cursor{0, 0u, 0u, 0u, 0u};
+    } else {
+      uint32_t lp, rip;
+      p.page_div.divmod(static_cast<uint32_t>(t0), lp, rip);
+      const int lpi = static_cast<int>(lp), r0 = static_cast<int>(rip);
+      const int last = p.n_table - 1;  // >= 0 whenever n_kv > 0
+      const int pg0 = p.table[min(lpi, last)];
+      const int pg1 = p.table[min(lpi + 1, last)];
+      asm volatile("" ::"s"(pg0), "s"(pg1));
+      const bool ok0 = lpi <= last && pg0 >= 0 && pg0 < p.pool_pages;
+      const bool ok1 = lpi + 1 <= last && pg1 >= 0 && pg1 < p.pool_pages;
+      const int split = p.page_tokens - r0;
+      // Bit masks rather than conditionals keep the compiler from branching around the multiplies.
+      const uint32_t m0 = 0u - static_cast<uint32_t>(ok0), m1 = 0u - static_cast<uint32_t>(ok1);
+      const int q0 = pg0 & static_cast<int>(m0), q1 = pg1 & static_cast<int>(m1);
+      const uint32_t far0 = static_cast<uint32_t>(kOutOfRange) & ~m0, far1 = static_cast<uint32_t>(kOutOfRange) & ~m1;
+      return Cursor{r0,
+                    (static_cast<uint32_t>((q0 * p.page_tokens + r0) * HD + h * D) & m0) | far0,
+                    (static_cast<uint32_t>((q1 * p.page_tokens - split) * HD + h * D) & m1) | far1,
+                    (static_cast<uint32_t>(((q0 * p.H + h) * p.page_tokens + r0) * 4) & m0) | far0,
+                    (static_cast<uint32_t>(((q1 * p.H + h) * p.page_tokens - split) * 4) & m1) | far1};
+    }
+  };
+  // The cursor of the tile after c's, at key t0n = c's + 64.  Within a page only the bases move: 64 rows
+  // of codes (64 H D bytes) and of scales (256 bytes) on both pages (split shrinks by 64).  A far base
+  // stays far: a page holds fewer than 2^31 bytes, so at most that much is added to kOutOfRange before
+  // the next page starts, below 2^32.
+  auto cursor_next = [&](const Cursor& c, int t0n) -> Cursor {
+    if constexpr (DENSE) {
+      (void)t0n;
+      return c;
+    } else {
+      if (c.r0 + BKV >= p.page_tokens) return cursor_at(t0n);
+      const uint32_t dc = static_cast<uint32_t>(BKV * HD), ds = static_cast<uint32_t>(BKV * 4);
+      return Cursor{c.r0 + BKV, c.cb0 + dc, c.cb1 + dc, c.sb0 + ds, c.sb1 + ds};
+    }
+  };
+
+  // Issue the loads of the tile starting at key t0 (cursor c).
+  auto load_tile = [&](int t0, const Cursor& c) {
+    if constexpr (DENSE) {
+      (void)c;
       const int key = min(t0 + skey, p.n_kv);
       const uint32_t off = static_cast<uint32_t>((key * static_cast<int>(p.ldkv) + h * D + schunk * 16) * 2) +
                            (key < p.n_kv ? 0u : static_cast<uint32_t>(kOutOfRange));
@@ -232,36 +288,12 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       sv0 = __builtin_amdgcn_raw_buffer_load_b128(rv, static_cast<int>(off), 0, 0);
       sv1 = __builtin_amdgcn_raw_buffer_load_b128(rv, static_cast<int>(off + 16), 0, 0);
     } else {
-      // Branch-free: past n_kv or on an invalid page the offsets are pushed
-      // beyond the buffer ranges (>= kOutOfRange > pool size), which read as zero.
-      // The page lookups are uniform across the workgroup, so both pages' base
-      // offsets are scalars; a lane only selects one and adds its own key's
-      // row offset (codes: skey * H * D + h * D + 16 schunk; scales: 4 skey).
-      uint32_t lp, rip;
-      p.page_div.divmod(static_cast<uint32_t>(t0), lp, rip);
-      const int lpi = static_cast<int>(lp), r0 = static_cast<int>(rip);
-      const int last = p.n_table - 1;  // >= 0 whenever n_kv > 0
-      const int pg0 = p.table[min(lpi, last)];
-      const int pg1 = p.table[min(lpi + 1, last)];
-      const bool ok0 = lpi <= last && pg0 >= 0 && pg0 < p.pool_pages;
-      const bool ok1 = lpi + 1 <= last && pg1 >= 0 && pg1 < p.pool_pages;
-      const int split = p.page_tokens - r0;
-      // Keys [0, split) of the tile sit on page pg0 from row r0, keys [split, 64) on pg1 from row 0.
-      // The bases are uint32: cb1 / sb1 wrap below zero when pg1 = 0 and a lane adds at least `split`
-      // rows back; an out-of-range base plus a row offset stays above every buffer range.  Bit masks
-      // rather than conditionals keep the compiler from branching around the multiplies.
-      const uint32_t m0 = 0u - static_cast<uint32_t>(ok0), m1 = 0u - static_cast<uint32_t>(ok1);
-      const int q0 = pg0 & static_cast<int>(m0), q1 = pg1 & static_cast<int>(m1);
-      const uint32_t far0 = static_cast<uint32_t>(kOutOfRange) & ~m0, far1 = static_cast<uint32_t>(kOutOfRange) & ~m1;
-      const uint32_t cb0 = (static_cast<uint32_t>((q0 * p.page_tokens + r0) * HD + h * D) & m0) | far0;
-      const uint32_t cb1 = (static_cast<uint32_t>((q1 * p.page_tokens - split) * HD + h * D) & m1) | far1;
-      const uint32_t sb0 = (static_cast<uint32_t>(((q0 * p.H + h) * p.page_tokens + r0) * 4) & m0) | far0;
-      const uint32_t sb1 = (static_cast<uint32_t>(((q1 * p.H + h) * p.page_tokens - split) * 4) & m1) | far1;
-      const bool first = skey < split;
+      // Branch-free: keys past n_kv are pushed out of range like an invalid page.
+      const bool first = skey < p.page_tokens - c.r0;
       const uint32_t lm = 0u - static_cast<uint32_t>(skey < p.n_kv - t0);   // all ones for keys before n_kv
       const uint32_t lfar = static_cast<uint32_t>(kOutOfRange) & ~lm;
-      const uint32_t co = (((first ? cb0 : cb1) + static_cast<uint32_t>(lane_co)) & lm) | lfar;
-      const uint32_t so = (((first ? sb0 : sb1) + static_cast<uint32_t>(lane_so)) & lm) | lfar;
+      const uint32_t co = (((first ? c.cb0 : c.cb1) + static_cast<uint32_t>(lane_co)) & lm) | lfar;
+      const uint32_t so = (((first ? c.sb0 : c.sb1) + static_cast<uint32_t>(lane_so)) & lm) | lfar;
       sk0 = __builtin_amdgcn_raw_buffer_load_b128(rk, static_cast<int>(co), 0, 0);
       sv0 = __builtin_amdgcn_raw_buffer_load_b128(rv, static_cast<int>(co), 0, 0);
       ssk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsk, static_cast<int>(so), 0, 0));
@@ -391,6 +423,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   float l_run = 0.f;        // this half's row sum (its 32 of every 64 keys)
 
   const int n_tiles = (p.n_kv + BKV - 1) / BKV;
+  Cursor cur_next{};  // the cursor of the tile loaded in the next iteration
 
   // One tile: scores with the staging of the next tile (into the other stage,
   // freed by the last barrier) and the loads of the one after; the column
@@ -465,7 +498,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
     // loads of the one after, and this tile's V^T operands (in flight
     // during the softmax).
     write_tile(cur ^ 1, nxt);
-    load_tile((it + 2) * BKV);
+    load_tile((it + 2) * BKV, cur_next);
     v8bf vf[4][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -535,13 +568,17 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t][db], pf, o[db], 0, 0, 0);
     }
+    cur_next = cursor_next(cur_next, (it + 3) * BKV);
     __syncthreads();
   };
 
   if (n_tiles > 0) {
-    load_tile(0);
+    cur_next = cursor_at(0);
+    load_tile(0, cur_next);
     store_tile(0);
-    load_tile(BKV);
+    cur_next = cursor_next(cur_next, BKV);
+    load_tile(BKV, cur_next);
+    cur_next = cursor_next(cur_next, 2 * BKV);
     __syncthreads();
     for (int it = 0; it + 1 < n_tiles; ++it) body(it, std::false_type{});
     body(n_tiles - 1, std::true_type{});
