@@ -202,9 +202,11 @@ def bench_block_linears(steps: int, warmup: int, dev: str):
     return {"ms": ms, "ops": ops, "tops": ops / (ms * 1e-3) / 1e12}
 
 
-def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8, quantized_qk: bool = False):
+def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8, quantized_qk: bool = False,
+                    zero_k: bool = False, zero_v: bool = False, warm_s: float = 0.0):
     """Paged FP8 attention: Q [4680, 12, 128] over `chunks` chunks (4680 keys each) of FP8 pages (with
-    ``quantized_qk``, the quantized-QK form: e4m3 queries against the K codes on the fp8 matrix cores)."""
+    ``quantized_qk``, the quantized-QK form: e4m3 queries against the K codes on the fp8 matrix cores).
+    ``zero_k`` / ``zero_v`` pack zeros in place of the N(0, 1) K / V (the same addresses and work)."""
     from waveforcing_amd.backend import attn_paged_fp8
     from waveforcing_amd.kv import PagedKV
 
@@ -216,14 +218,27 @@ def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8, quantize
     g = torch.Generator().manual_seed(12)
     k = torch.randn((n_kv, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
     v = torch.randn((n_kv, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
-    pool.pack(k, v, table)
+    pool.pack(torch.zeros_like(k) if zero_k else k, torch.zeros_like(v) if zero_v else v, table)
     del k, v
     q = torch.randn((TOKENS, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
     ctx = PagedKV(pool, table, n_kv)
     out = torch.empty_like(q)
-    ms = _timed(lambda: attn_paged_fp8(q, ctx, out=out, quantized_qk=quantized_qk), steps, warmup)
+    ms = _timed(lambda: attn_paged_fp8(q, ctx, out=out, quantized_qk=quantized_qk), steps, warmup, warm_s)
     flops = 4.0 * TOKENS * n_kv * H * HEAD_DIM
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops, "keys": n_kv}
+
+
+def bench_attention_data(steps: int, warmup: int, dev: str, repeats: int = 2):
+    """Both attention forms on the attention workload with N(0, 1) or zero K / V in the pages, each timed
+    after a second of sustained launches: the clock under this load depends on the operand values."""
+    res = {}
+    for rep in range(repeats):
+        for name, zk, zv in (("randn", False, False), ("zero", True, True), ("zero_k", True, False),
+                             ("zero_v", False, True)):
+            for qk in (False, True):
+                r = bench_attention(steps, warmup, dev, quantized_qk=qk, zero_k=zk, zero_v=zv, warm_s=1.0)
+                res[f"{name}{'_qk8' if qk else ''}_ms_{rep}"] = round(r["ms"], 4)
+    return res
 
 
 def bench_block(scale: str, steps: int, warmup: int, dev: str, quantized_qk: bool = False):
@@ -625,7 +640,7 @@ def main() -> None:
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
                                        "tick_1p3b", "generate_1p3b", "copy", "attention_qk8", "block_1p3b_qk8",
-                                       "kv_pertensor"],
+                                       "kv_pertensor", "attention_data"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -648,7 +663,7 @@ def main() -> None:
               "generate_1p3b": bench_generate,
               "attention_qk8": lambda s, w, d: bench_attention(s, w, d, quantized_qk=True),
               "block_1p3b_qk8": lambda s, w, d: bench_block("1.3b", s, w, d, quantized_qk=True),
-              "kv_pertensor": bench_kv_pertensor,
+              "kv_pertensor": bench_kv_pertensor, "attention_data": bench_attention_data,
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return
