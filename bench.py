@@ -175,6 +175,30 @@ def bench_gemm(steps: int, warmup: int, dev: str):
             "ms_fp8_linear": ms_f8_lin, "tops_fp8_linear": ops / (ms_f8_lin * 1e-3) / 1e12}
 
 
+def bench_gemm_data(steps: int, warmup: int, dev: str):
+    """The int8 GEMM with uniform random int8 operands, and with A or W all zero (the same instructions, addresses
+    and bytes), each timed after a second of sustained launches, at the 1.3B linear, 14B fc_out and 14B QKV
+    shapes: the clock under this load depends on the operand values."""
+    from waveforcing_amd.fp8 import gemm_i8
+
+    g = torch.Generator().manual_seed(1)
+    res = {}
+    for name, M, N, K in (("1p3b_linear", TOKENS, 1536, 1536), ("14b_fc_out", TOKENS, 5120, 13824),
+                          ("14b_qkv", TOKENS, 15360, 5120)):
+        a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+        w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+        sx = (torch.rand(M, generator=g) * 0.01).to(dev)
+        sw = (torch.rand(N, generator=g) * 0.01).to(dev)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        reps = 20 if K < 5000 else 5
+        for tag, aa, ww in (("rand", a, w), ("zero_a", torch.zeros_like(a), w), ("zero_w", a, torch.zeros_like(w))):
+            ms = _timed(lambda: [gemm_i8(aa, ww, sx, sw, None, out=y) for _ in range(reps)], steps, warmup, 1.0) / reps
+            res[f"{name}_{tag}_us"] = round(ms * 1e3, 2)
+            res[f"{name}_{tag}_tops"] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)
+        del a, w, y
+    return res
+
+
 def bench_block_linears(steps: int, warmup: int, dev: str):
     """The Wan-1.3B block's W8A8 GEMMs on one 4680-token chunk as the block runs them: fused QKV [4608, 1536],
     O [1536, 1536], fc_in [8960, 1536], fc_out [1536, 8960] (activations pre-quantized; 345.97 G int8 ops per
@@ -640,7 +664,7 @@ def main() -> None:
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
                                        "tick_1p3b", "generate_1p3b", "copy", "attention_qk8", "block_1p3b_qk8",
-                                       "kv_pertensor", "attention_data"],
+                                       "kv_pertensor", "attention_data", "gemm_data"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -664,6 +688,7 @@ def main() -> None:
               "attention_qk8": lambda s, w, d: bench_attention(s, w, d, quantized_qk=True),
               "block_1p3b_qk8": lambda s, w, d: bench_block("1.3b", s, w, d, quantized_qk=True),
               "kv_pertensor": bench_kv_pertensor, "attention_data": bench_attention_data,
+              "gemm_data": bench_gemm_data,
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
         print(json.dumps({"only": args.only, **fn(args.steps, args.warmup, dev)}), flush=True)
         return

@@ -55,10 +55,10 @@
 //    4-7 % faster on every multi-round Wan shape.
 //
 // Phase timing (built only with -DWF_GEMM_PHASES, never in the product library): the first and the
-// fifth wave of every workgroup (the two waves of SIMD 0) record the shader clock (s_memtime) at kernel
-// entry, after the prologue barrier, after the K loop's last barrier and after the epilogue's last
-// store, into a buffer registered with wf_gemm_set_phase_buffer: 8 stamps per workgroup,
-// [wave 0: 4][wave 4: 4].  waveforcing_amd/gemm_phases.py builds that variant and summarizes the
+// fifth wave of every workgroup (the two waves of SIMD 0) record, at kernel entry, after the prologue
+// barrier, after the K loop's last barrier and after the epilogue's last store, the shader clock
+// (s_memtime, wave 0) and the 100 MHz reference clock (s_memrealtime, wave 4) into a buffer registered
+// with wf_gemm_set_phase_buffer: 8 stamps per workgroup, [wave 0: 4][wave 4: 4].  waveforcing_amd/gemm_phases.py builds that variant and summarizes the
 // stamps (prologue, cycles per K step, epilogue).
 #include <type_traits>
 #include <utility>
@@ -167,7 +167,9 @@ struct GemmArgs {
 __device__ inline void phase_stamp(const GemmArgs& p, int wave, int lane, int slot) {
 #ifdef WF_GEMM_PHASES
   if (p.phases != nullptr && (wave == 0 || wave == NW / 2)) {
-    const uint64_t t = __builtin_amdgcn_s_memtime();
+    // wave 0: the shader clock (cycles); its SIMD mate: the constant 100 MHz reference clock at the same
+    // points (the same barriers), which turns the cycle counts into a frequency
+    const uint64_t t = wave == 0 ? __builtin_amdgcn_s_memtime() : __builtin_amdgcn_s_memrealtime();
     if (lane == 0) p.phases[static_cast<int64_t>(blockIdx.x) * 8 + (wave == 0 ? 0 : 4) + slot] = t;
   }
 #else

@@ -5,13 +5,17 @@ Usage: python -m waveforcing_amd.build --variant gemm_phases   (on the CPU, once
 
 The instrumented library (libwf_mi355x_gemm_phases.so, built with
 -DWF_GEMM_PHASES) has the same kernels as the product library plus shader-clock
-stamps (s_memtime) that the two waves of SIMD 0 of every workgroup write at
-kernel entry, after the prologue barrier, after the K loop's last barrier and
-after the epilogue's last store.  For each Wan shape this prints, averaged over
+stamps that the two waves of SIMD 0 of every workgroup write at kernel entry,
+after the prologue barrier, after the K loop's last barrier and after the
+epilogue's last store: the shader clock (s_memtime, wave 0) and the 100 MHz
+reference clock (s_memrealtime, wave 4).  For each Wan shape this prints, averaged over
 the workgroups of R launches (wave 0's stamps): the prologue, the cycles per K step (the K loop
 divided by its steps, against the 1024 cycles one step needs on the matrix
 cores: 16 v_mfma_i32_32x32x32_i8 of 32 cycles for each of the SIMD's two
-waves) and the epilogue, with the launch's event time.  Stamps are compared
+waves) and the epilogue, with the launch's event time and the shader clock (a workgroup's
+cycles over its reference-clock time, averaged).
+With --zero-a the activations are all zero: the same instructions, addresses and bytes, fewer
+toggling bits, so the cycle counts stay and only the clock under the power limit moves.  Stamps are compared
 only within a workgroup: the shader-clock counters of different XCDs are not
 one time base.
 """
@@ -21,6 +25,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import math
+import time
 
 import torch
 
@@ -41,9 +46,11 @@ def _lib(path: str | None = None):
     return lib
 
 
-def measure(lib, M: int, N: int, K: int, reps: int, dev="cuda:0") -> dict:
+def measure(lib, M: int, N: int, K: int, reps: int, dev="cuda:0", zero_a: bool = False) -> dict:
     g = torch.Generator(device=dev).manual_seed(M + N + K)
     qx = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    if zero_a:
+        qx.zero_()
     qw = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
     sx = torch.rand((M,), generator=g, device=dev) * 1e-3
     sw = torch.rand((N,), generator=g, device=dev) * 1e-3
@@ -61,8 +68,14 @@ def measure(lib, M: int, N: int, K: int, reps: int, dev="cuda:0") -> dict:
             raise RuntimeError(f"wf_gemm_i8 failed with status {rc}")
 
     lib.wf_gemm_set_phase_buffer(None)
-    for _ in range(5):
+    t0 = time.perf_counter()
+    n = 0
+    while n < 5 or time.perf_counter() - t0 < 0.5:  # half a second of sustained launches: the clock settles
         launch()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
     lib.wf_gemm_set_phase_buffer(stamps.data_ptr())
     rows, times = [], []
     for _ in range(reps):
@@ -76,16 +89,19 @@ def measure(lib, M: int, N: int, K: int, reps: int, dev="cuda:0") -> dict:
         rows.append(stamps.cpu())
     lib.wf_gemm_set_phase_buffer(None)
     nk = math.ceil(K / BK)
-    pro, step, epi = [], [], []
+    pro, step, epi, life = [], [], [], []
     for st in rows:
-        live = st[(st[:, 0:4] > 0).all(dim=1)].double()
+        live = st[(st > 0).all(dim=1)].double()
         w0 = live[:, 0:4]
         pro.append((w0[:, 1] - w0[:, 0]).mean().item())
         step.append(((w0[:, 2] - w0[:, 1]) / nk).mean().item())
         epi.append((w0[:, 3] - w0[:, 2]).mean().item())
+        ref = live[:, 4:8]
+        life.append(((w0[:, 3] - w0[:, 0]) / ((ref[:, 3] - ref[:, 0]) * 1e-8)).mean().item())
     mean = lambda v: sum(v) / len(v)  # noqa: E731
     return {"tiles": tiles, "k_steps": nk, "prologue_cycles": mean(pro), "cycles_per_k_step": mean(step),
-            "epilogue_cycles": mean(epi), "event_us": mean(times) * 1e6, "mfma_cycles_per_k_step": 1024}
+            "epilogue_cycles": mean(epi), "event_us": mean(times) * 1e6, "mfma_cycles_per_k_step": 1024,
+            "clock_ghz": mean(life) / 1e9}
 
 
 def main() -> None:
@@ -94,16 +110,18 @@ def main() -> None:
     ap.add_argument("--lib", default=None, help="another library built with -DWF_GEMM_PHASES (default: the "
                                                 "gemm_phases variant of this package)")
     ap.add_argument("--shapes", default=None, help="comma-separated indices into the shape list")
+    ap.add_argument("--zero-a", action="store_true", help="all-zero activations (same work, fewer toggling bits)")
     args = ap.parse_args()
     lib = _lib(args.lib)
     shapes = SHAPES if args.shapes is None else [SHAPES[int(i)] for i in args.shapes.split(",")]
     print("| shape | M x N x K | tiles | K steps | prologue (cycles) | cycles / K step (MFMA: 1024) | "
-          "epilogue (cycles) | event µs |")
-    print("|---|---|---:|---:|---:|---:|---:|---:|")
+          "epilogue (cycles) | event µs | clock (GHz) |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|")
     for name, M, N, K in shapes:
-        r = measure(lib, M, N, K, args.reps)
+        r = measure(lib, M, N, K, args.reps, zero_a=args.zero_a)
         print(f"| {name} | {M} x {N} x {K} | {r['tiles']} | {r['k_steps']} | {r['prologue_cycles']:.0f} | "
-              f"{r['cycles_per_k_step']:.0f} | {r['epilogue_cycles']:.0f} | {r['event_us']:.2f} |", flush=True)
+              f"{r['cycles_per_k_step']:.0f} | {r['epilogue_cycles']:.0f} | {r['event_us']:.2f} | "
+              f"{r['clock_ghz']:.2f} |", flush=True)
 
 
 if __name__ == "__main__":
