@@ -707,6 +707,8 @@ def main() -> None:
     stk14 = bench_stack(3, 1, dev, "14b")
     dit = bench_dit(max(3, args.steps // 10), 1, dev)
     gen = bench_generate(1, 1, dev)
+    gdat = bench_gemm_data(max(3, args.steps // 20), 2, dev)
+    adat = bench_attention_data(max(5, args.steps // 5), 2, dev, repeats=1)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     cpu_extra = None if args.no_cpu_baseline else cpu_baseline_extra()
     # one launch per step: the launch duration is the step time
@@ -820,6 +822,13 @@ def main() -> None:
             "dit_block_note": "one block, 4680-token 3-frame chunk, 37440-key FP8 paged self-attn context, "
                               "512-token text cross-attn, all linears W8A8 int8, random init; includes a 9.4/31 MB "
                               "copy to reset x each step",
+            "w8a8_gemm_power": {**gdat, "note": "the int8 GEMM on uniform random int8 operands and with A or W all "
+                                                "zero (the same instructions, addresses and bytes), each after a "
+                                                "second of sustained launches: the clock under the power limit "
+                                                "depends on the operands' switching"},
+            "attn_power": {**{k.replace("_ms_0", "_ms"): v for k, v in adat.items()},
+                           "note": "both attention forms on the attention workload with N(0,1) or zero K / V in the "
+                                   "pages, each after a second of sustained launches"},
         },
     }
     print(json.dumps(line), flush=True)
