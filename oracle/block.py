@@ -88,7 +88,7 @@ def rope_apply_table(x, cos, sin):
 
 
 def block_forward(p, x, e, grid, start_frame, pool_k, pool_v, context_table, own_table, n_context, page_tokens,
-                  text_k, text_v, heads, return_unroped_k=False):
+                  text_k, text_v, heads, return_unroped_k=False, paged_attn=None):
     """One block on the CPU.
 
     p: waveforcing_amd.block.BlockParams (CPU bf16); x [T, dim] bf16;
@@ -97,7 +97,9 @@ def block_forward(p, x, e, grid, start_frame, pool_k, pool_v, context_table, own
     which this chunk's K/V are packed at own_table (modified in place);
     text_k / text_v [L, H, D] bf16.  Returns the new x, and with
     ``return_unroped_k`` also the chunk's normalized, un-rotated K [T, H, D]
-    (the exchange's unroped_key).
+    (the exchange's unroped_key).  ``paged_attn`` replaces the self-attention
+    over the pages (default :func:`oracle.attention.paged_fp8`; the reference
+    swaps its attention function the same way, backend.py:141-148).
     """
     T, dim = x.shape
     frames, height, width = grid
@@ -122,7 +124,7 @@ def block_forward(p, x, e, grid, start_frame, pool_k, pool_v, context_table, own
     k = rope_apply(ku, ang)
     okv.pack(k, own_table, page_tokens, *pool_k)
     okv.pack(v, own_table, page_tokens, *pool_v)
-    y = oat.paged_fp8(q, pool_k, pool_v, context_table, n_context, page_tokens).to(torch.bfloat16)
+    y = (paged_attn or oat.paged_fp8)(q, pool_k, pool_v, context_table, n_context, page_tokens).to(torch.bfloat16)
     y = lin(y.reshape(T, dim), p.o_w, p.o_b)
     x = x + y * per_frame(y, 2)
 

@@ -10,7 +10,10 @@ L2 error of the block output <= 1e-2 and max |diff| <= 5e-2 * max |x|:
 * at 1.3B widths (dim 1536, 12 heads, FFN 8960) on a small chunk geometry;
 * on a whole 1.3B chunk: 3 x 30 x 52 = 4680 tokens, 1560-token pages, 7
   prior chunks of FP8 context (37440 keys with its own) and 512 text tokens;
-* on a whole 14B chunk (dim 5120, 40 heads, FFN 13824) in the same setting.
+* on a whole 14B chunk (dim 5120, 40 heads, FFN 13824) in the same setting;
+* on a whole 1.3B chunk through the ``hip_fp8_qk`` backend (quantized QK,
+  the counterpart of the reference's Sage path) against the oracle block
+  with the quantized-QK attention.
 
 The wiring probes of tests/block_probes.py null every path where the two
 sides' arithmetic differs except the GELU, so the GPU block must equal their
@@ -27,9 +30,11 @@ import pytest
 import torch
 
 import block_probes as bp
+from oracle import attention as oat
 from oracle import block as ob
 from oracle import kv as okv
 from waveforcing_amd import rope
+from waveforcing_amd.backend import _WAVE_STATE, enable_hip_fp8, enable_hip_fp8_qk
 from waveforcing_amd.block import QuantizedWanBlock, random_block_params
 from waveforcing_amd.kv import Fp8PagePool
 
@@ -59,10 +64,10 @@ def _case(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed):
                 P=P, prior_ids=prior_ids, own_ids=own_ids, ctx_ids=ctx_ids, n_ctx=n_ctx, start_frame=start_frame)
 
 
-def _compare(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed):
+def _compare(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed, quantized_qk=False):
     c = _case(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed)
-    print(f"\n[case] dim {dim} heads {heads} ffn {ffn} tokens {c['T']} context {c['n_ctx']} text {text_len}",
-          flush=True)
+    print(f"\n[case] dim {dim} heads {heads} ffn {ffn} tokens {c['T']} context {c['n_ctx']} text {text_len}"
+          f"{' quantized QK' if quantized_qk else ''}", flush=True)
     # GPU
     blk = QuantizedWanBlock(c["params"], heads, DEV)
     pool = Fp8PagePool(c["P"], heads, 128, c["page"], DEV)
@@ -70,8 +75,14 @@ def _compare(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed):
     tk, tv = blk.text_kv(c["context"].to(DEV))
     cos, sin = rope.cos_sin(frames, h, w, c["start_frame"], device=DEV)
     x_gpu = c["x"].to(DEV).clone()
-    blk.forward(x_gpu, c["e"].to(DEV), cos, sin, pool, pool.page_table(c["ctx_ids"]), pool.page_table(c["own_ids"]),
-                c["n_ctx"], (tk, tv))
+    saved = dict(_WAVE_STATE)
+    try:
+        (enable_hip_fp8_qk if quantized_qk else enable_hip_fp8)()
+        blk.forward(x_gpu, c["e"].to(DEV), cos, sin, pool, pool.page_table(c["ctx_ids"]),
+                    pool.page_table(c["own_ids"]), c["n_ctx"], (tk, tv))
+    finally:
+        _WAVE_STATE.clear()
+        _WAVE_STATE.update(saved)
     out = x_gpu.cpu().double()
     own_k = pool.k_codes[c["own_ids"]].cpu()
     del blk, pool, x_gpu
@@ -84,7 +95,8 @@ def _compare(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed):
     otk, otv = ob.text_kv(c["params"], c["context"], heads)
     tk_err = (tk.cpu().double() - otk.double()).abs().max().item()
     ref = ob.block_forward(c["params"], c["x"], c["e"], (frames, h, w), c["start_frame"], pk, pv, c["ctx_ids"],
-                           c["own_ids"], c["n_ctx"], c["page"], otk, otv, heads).double()
+                           c["own_ids"], c["n_ctx"], c["page"], otk, otv, heads,
+                           paged_attn=oat.paged_fp8_qk8 if quantized_qk else None).double()
     codes_same = (own_k == pk[0][c["own_ids"]]).double().mean().item()
     rel = ((out - ref).norm() / ref.norm()).item()
     mx = (out - ref).abs().max().item()
@@ -104,6 +116,12 @@ def test_block_1p3b_whole_chunk_matches_oracle():
 
 def test_block_14b_whole_chunk_matches_oracle():
     _compare(5120, 40, 13824, 3, 30, 52, prior_chunks=7, text_len=512, seed=7)
+
+
+def test_block_1p3b_whole_chunk_quantized_qk_matches_oracle():
+    """The block through the hip_fp8_qk backend (the counterpart of the reference's Sage path) against the
+    oracle block with the quantized-QK attention, same bar."""
+    _compare(1536, 12, 8960, 3, 30, 52, prior_chunks=7, text_len=512, seed=8, quantized_qk=True)
 
 
 @pytest.mark.parametrize("kind", ["residuals", "attn_mod", "cross", "ffn_mod", "self_qk", "cross_q"])
