@@ -46,16 +46,17 @@ def paged_fp8(q, k_pool, v_pool, table: Sequence[int], n_kv: int, page_tokens: i
 
 
 def quantize_q_rows(q: torch.Tensor):
-    """e4m3 quantization of each query row (per head): s_q = amax|q| / 448 in fp32 (1 for an all-zero row) and
-    codes e4m3(clamp(q * (448 / amax), +-448)), where 448 / amax is the correctly rounded fp32 quotient (taken
-    through float64: torch's CPU scalar / tensor goes through the reciprocal and can land one ulp off, which
-    moves codes that sit on an e4m3 rounding tie).  q [Lq, H, D] bf16 -> (fp32 decoded codes [Lq, H, D],
-    s_q [Lq, H])."""
+    """e4m3 quantization of each query row (per head) with a power-of-two scale: s_q = 2^e, the smallest power
+    of two with amax|q| <= 448 s_q (1 for an all-zero row), and codes e4m3(q / s_q), where the division by a power
+    of two is exact, so each code is the e4m3 rounding (to nearest, ties to even) of q 2^-e itself.
+    q [Lq, H, D] bf16 -> (fp32 decoded codes [Lq, H, D], s_q [Lq, H])."""
     qf = q.float()
     amax = qf.abs().amax(dim=-1)
-    inv = torch.where(amax > 0, (448.0 / amax.double()).float(), torch.zeros_like(amax))
-    s_q = torch.where(amax > 0, amax * (1.0 / 448.0), torch.ones_like(amax))
-    codes = (qf * inv[..., None]).clamp(-448.0, 448.0).to(okv.FP8).float()
+    mant, expo = torch.frexp(amax.double())            # amax = mant 2^expo, mant in [0.5, 1)
+    e = torch.where(mant <= 0.875, expo - 9, expo - 8)  # 448 = 0.875 2^9
+    e = torch.where(amax > 0, e, torch.zeros_like(e)).clamp(-127, 127)
+    s_q = torch.pow(2.0, e.double()).float()
+    codes = torch.ldexp(qf.double(), -e[..., None].double()).clamp(-448.0, 448.0).float().to(okv.FP8).float()
     return codes, s_q
 
 

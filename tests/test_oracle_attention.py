@@ -10,8 +10,10 @@ The quantized-QK form (paged_fp8_qk8): queries whose rows are already e4m3
 values times a power of two (amax = 448 * 2^k) pass the quantization
 unchanged, so the form reduces to the exact paged attention; a single key
 returns its V row; all-zero queries give the mean of V; each query row's
-codes are within half an e4m3 step of q * 448 / amax; and on N(0, 1) data the
-form stays within the attention bar of the exact one while differing from it.
+scale is the smallest power of two with amax <= 448 s_q, so its largest code
+lies in [224, 448], and every code is the e4m3 rounding of q / s_q (ties to
+even, checked on exact ties); and on N(0, 1) data the form stays within the
+attention bar of the exact one while differing from it.
 """
 
 import math
@@ -117,18 +119,27 @@ def test_qk8_closed_forms_and_error_scale():
     zero = oat.paged_fp8_qk8(torch.zeros((4, 3, 128), dtype=torch.bfloat16), kp, vp, ids, 200, 64)
     mean = okv.unpack(ids, 200, 64, *vp).double().mean(0).float()
     assert (zero - mean).abs().max().item() < 1e-6
-    # codes within half an e4m3 step (2^-4 relative) of q * 448 / amax
+    # power-of-two scales: the smallest with amax <= 448 s_q, so every row's largest value lies in (224, 448] s_q
+    # (its code in [224, 448] after rounding), and codes within half an e4m3 step (2^-4 relative) of q / s_q
     q = _rand((64, 3, 128), 19)
     qc, sq = oat.quantize_q_rows(q)
+    mant, _ = torch.frexp(sq)
+    assert (mant == 0.5).all()
+    row_max = qc.abs().amax(dim=-1)
+    assert ((row_max >= 224.0) & (row_max <= 448.0)).all()
+    assert (q.float().abs().amax(dim=-1) <= 448.0 * sq).all() and (q.float().abs().amax(dim=-1) > 224.0 * sq).all()
     ideal = q.float() / sq[..., None]
     assert ((qc - ideal).abs() <= ideal.abs() * 2.0 ** -4 + 2.0 ** -10).all()
-    assert qc.abs().amax().item() == 448.0
-    # 448 / amax is the correctly rounded fp32 quotient: with amax 3 and an element 1.125 the quotient is
-    # RN32(448 / 3) * 1.125 = 168 exactly, an e4m3 tie between 160 and 176 that rounds to even (160);
-    # torch's 448.0 / tensor(3.0) is one ulp above and would give 176
+    # amax 3 takes s_q = 2^-7 (3 * 2^7 = 384 <= 448 < 768); 1.0625 * 2^7 = 136 is an e4m3 tie between 128 and 144
+    # and 1.1875 * 2^7 = 152 one between 144 and 160: ties go to the even code (128, 160); amax 448 keeps s_q = 1
     tie = torch.zeros((1, 1, 128), dtype=torch.bfloat16)
-    tie[0, 0, 0], tie[0, 0, 1] = 3.0, 1.125
-    assert float(oat.quantize_q_rows(tie)[0][0, 0, 1]) == 160.0
+    tie[0, 0, 0], tie[0, 0, 1], tie[0, 0, 2] = 3.0, 1.0625, 1.1875
+    tc, ts = oat.quantize_q_rows(tie)
+    assert float(ts[0, 0]) == 2.0 ** -7 and tc[0, 0, :3].tolist() == [384.0, 128.0, 160.0]
+    top = torch.zeros((1, 1, 128), dtype=torch.bfloat16)
+    top[0, 0, 5] = -448.0
+    tc, ts = oat.quantize_q_rows(top)
+    assert float(ts[0, 0]) == 1.0 and float(tc[0, 0, 5]) == -448.0
     got = oat.paged_fp8_qk8(q, kp, vp, ids, 200, 64)
     exact = oat.paged_fp8(q, kp, vp, ids, 200, 64)
     err = (got - exact).abs().max().item()

@@ -160,10 +160,13 @@ __device__ inline float pair_sum(float v) {
 }
 
 // QK8: the quantized-QK form (the counterpart of the reference's SageAttention backend, backend.py:57-62,
-// 144-146).  Each query is quantized once to e4m3 with its own scale s_q = amax|q| / 448, the e4m3 K codes of the
+// 144-146).  Each query is quantized once to e4m3 with a power-of-two scale s_q = 2^e_q, the smallest with
+// amax|q| <= 448 s_q (the codes are the e4m3 rounding of q 2^-e_q, an exact scaling), the e4m3 K codes of the
 // pages are used as they are, and S^T = K_codes Q_codes^T runs on the fp8 matrix cores
-// (v_mfma_f32_32x32x64_f8f6f4); every score is then multiplied by its key's s_k, and s_q joins the softmax
-// scale in the exponent's FMA.  V and P stay exact as in the bf16 form.
+// (v_mfma_scale_f32_32x32x64_f8f6f4), which apply 2^e_q to each query's column as its block scale.  The
+// staging stores u_k = s_k * softmax scale * log2(e) per key, the same for every query, so a score's exponent
+// is one FMA, s'' u_k - m; the tile's maximum is bounded by max s'' * max u_k (exact maxima only in the rare
+// rescale).  V and P stay exact as in the bf16 form.
 template <bool DENSE, bool QK8>
 __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) {
   static_assert(!(DENSE && QK8), "the quantized-QK form reads FP8 pages");
@@ -305,9 +308,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // write into LDS stage `buf`.
   auto dequant_tile = [&](uint4* out) {
     if constexpr (QK8) {
-      // K codes as they are, the K scale alongside; V as in the bf16 form
+      // K codes as they are, the key's exponent factor u_k = s_k * softmax scale * log2(e) alongside; V as in
+      // the bf16 form
       out[0] = make_uint4(sk0[0], sk0[1], sk0[2], sk0[3]);
-      out[1] = make_uint4(__builtin_bit_cast(uint32_t, ssk), 0u, 0u, 0u);
+      out[1] = make_uint4(__builtin_bit_cast(uint32_t, __fmul_rn(ssk, p.qk_scale)), 0u, 0u, 0u);
       const uint2 e = dequant4_bf16(sv0[0], ssv), f = dequant4_bf16(sv0[1], ssv);
       const uint2 g = dequant4_bf16(sv0[2], ssv), i = dequant4_bf16(sv0[3], ssv);
       out[2] = make_uint4(e.x, e.y, f.x, f.y);
@@ -350,7 +354,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // ---- Q^T fragments for this wave's 32 queries (kept for the whole kernel)
   v8bf qf[QK8 ? 1 : 8];
   v8i qc[2];             // QK8: e4m3 codes of d = 64 m + 32 half + 0..31 (m = 0, 1)
-  float cq = p.qk_scale;  // the exponent's scale: softmax scale * log2(e), times s_q in the QK8 form
+  int q_scale = 127;     // QK8: the query's block scale for the MFMA, E8M0 (127 + e_q)
   if constexpr (QK8) {
     // lane (l32, half) holds d = 64 m + 32 half + 0..31 of query l32, the K positions its fp8 operand bytes
     // stand for (the K fragments below use the same assignment)
@@ -373,9 +377,16 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo_to_f32(w[e])), fabsf(bf16_hi_to_f32(w[e]))));
     }
     amax = pair_max(amax);
-    const float inv = amax > 0.f ? 448.0f / amax : 0.f;
-    cq = (amax > 0.f ? amax * (1.0f / 448.0f) : 1.0f) * p.qk_scale;
-    auto code = [&](float v) { return fminf(fmaxf(v * inv, -448.0f), 448.0f); };
+    // e_q: amax = f 2^E with f in [0.5, 1); amax <= 448 2^e (448 = 0.875 2^9) holds from e = E - 9 when
+    // f <= 0.875, else from e = E - 8.  A zero row keeps e_q = 0 (all codes zero).
+    int e_q = 0;
+    if (amax > 0.f) {
+      const int E = __builtin_amdgcn_frexp_expf(amax);
+      e_q = __builtin_amdgcn_frexp_mantf(amax) <= 0.875f ? E - 9 : E - 8;
+      e_q = min(max(e_q, -127), 127);  // the E8M0 range
+    }
+    q_scale = 127 + e_q;
+    auto code = [&](float v) { return fminf(fmaxf(__builtin_ldexpf(v, -e_q), -448.0f), 448.0f); };
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       uint32_t c8[8];
@@ -416,8 +427,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   v16f o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  const float c = cq;
-  float m_use = -INFINITY;  // maximum used in the exponents (raw score units)
+  // Softmax state.  The bf16 form keeps its maxima in raw score units and scales by c in the exponent's
+  // FMA; the QK8 form's scores enter the exponent through u_k, so its maxima are in exponent units (c = 1).
+  const float c = QK8 ? 1.0f : p.qk_scale;
+  float m_use = -INFINITY;  // maximum used in the exponents
   float m_thr = -INFINITY;  // rescale when a tile's maximum exceeds this
   float neg_mc = 0.f;       // -m_use * c
   float l_run = 0.f;        // this half's row sum (its 32 of every 64 keys)
@@ -437,7 +450,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
 
     uint4 nxt[4];
     v16f s[2];
-    float4 skv[2][4];  // QK8: s_k of the lane's keys 32 b + 8 g + 4 half + 0..3
+    float4 skv[2][4];  // QK8: u_k of the lane's keys 32 b + 8 g + 4 half + 0..3
     if constexpr (QK8) {
       // K code fragments (32 bytes per MFMA: d = 64 m + 32 half + 0..31 of key 32 b + l32) and the lane's
       // key scales (the same 16 per half-wave: broadcast reads), all in flight before the first MFMA
@@ -463,7 +476,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       for (int m = 0; m < 2; ++m)
 #pragma unroll
         for (int b = 0; b < 2; ++b)
-          s[b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf8[b][m], qc[m], s[b], 0, 0, 0, 0, 0, 0);
+          s[b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf8[b][m], qc[m], s[b], 0, 0, 0, 127, 0, q_scale);
       __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the 8 K-fragment and 8 scale reads first
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -510,16 +523,18 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
         vf[t][db] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
 
+    // QK8: u_k of the lane's 32 keys as an array (element 4 g + e of block b), 1 for keys past n_kv (whose
+    // scale reads as zero: their masked score of -inf then still yields a zero weight)
+    float u[2][16];
     if constexpr (QK8) {
-      // each score times its key's scale
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          s[b][4 * g] *= skv[b][g].x;
-          s[b][4 * g + 1] *= skv[b][g].y;
-          s[b][4 * g + 2] *= skv[b][g].z;
-          s[b][4 * g + 3] *= skv[b][g].w;
+          u[b][4 * g] = skv[b][g].x;
+          u[b][4 * g + 1] = skv[b][g].y;
+          u[b][4 * g + 2] = skv[b][g].z;
+          u[b][4 * g + 3] = skv[b][g].w;
         }
     }
     if constexpr (decltype(LAST)::value) {
@@ -529,17 +544,38 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            s[b][4 * g + e] = key_base + b * 32 + g * 8 + half * 4 + e >= p.n_kv ? -INFINITY : s[b][4 * g + e];
+          for (int e = 0; e < 4; ++e) {
+            const bool past = key_base + b * 32 + g * 8 + half * 4 + e >= p.n_kv;
+            s[b][4 * g + e] = past ? -INFINITY : s[b][4 * g + e];
+            if constexpr (QK8) u[b][4 * g + e] = past ? 1.0f : u[b][4 * g + e];
+          }
     }
     float mt = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[b][e]);
+    if constexpr (QK8) {
+      // an upper bound of the half's largest exponent s'' u_k: max s'' times the largest u_k when max s'' >= 0,
+      // else 0 (every exponent is negative); the exact maximum is taken only when the bound asks for a rescale
+      float um = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) um = fmaxf(um, u[b][e]);
+      mt = mt >= 0.f ? mt * um : 0.f;
+    }
     mt = pair_max(mt);
-    // exponents in base 2: p = 2^(c * (s - m_use)), c = softmax_scale * log2(e) >= 0
+    // exponents in base 2: p = 2^(c * (s - m_use)), c = softmax_scale * log2(e) >= 0 (QK8: 2^(s'' u_k - m_use))
     if (__ballot(mt > m_thr)) {
+      if constexpr (QK8) {
+        float ex = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) ex = fmaxf(ex, s[b][e] * u[b][e]);
+        mt = pair_max(ex);
+      }
       const float m_new = fmaxf(m_use, mt);
       const float alpha = (m_use == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(c * (m_use - m_new));
 #pragma unroll
@@ -558,8 +594,13 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pv[e] = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g0 + e], c, neg_mc));
-        pv[4 + e] = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g0 + 4 + e], c, neg_mc));
+        if constexpr (QK8) {
+          pv[e] = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g0 + e], u[b][4 * g0 + e], neg_mc));
+          pv[4 + e] = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g0 + 4 + e], u[b][4 * g0 + 4 + e], neg_mc));
+        } else {
+          pv[e] = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g0 + e], c, neg_mc));
+          pv[4 + e] = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g0 + 4 + e], c, neg_mc));
+        }
       }
       const uint32_t w0 = cvt_bf16x2(pv[0], pv[1]), w1 = cvt_bf16x2(pv[2], pv[3]);
       const uint32_t w2 = cvt_bf16x2(pv[4], pv[5]), w3 = cvt_bf16x2(pv[6], pv[7]);
