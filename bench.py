@@ -226,11 +226,15 @@ def bench_block_linears(steps: int, warmup: int, dev: str):
     return {"ms": ms, "ops": ops, "tops": ops / (ms * 1e-3) / 1e12}
 
 
-def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8, quantized_qk: bool = False,
+ATTN_FORMS = {"bf16": {}, "qk8": {"quantized_qk": True}, "qkpv8": {"fp8_pv": True}}
+
+
+def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8, form: str = "bf16",
                     zero_k: bool = False, zero_v: bool = False, warm_s: float = 0.0):
-    """Paged FP8 attention: Q [4680, 12, 128] over `chunks` chunks (4680 keys each) of FP8 pages (with
-    ``quantized_qk``, the quantized-QK form: e4m3 queries against the K codes on the fp8 matrix cores).
-    ``zero_k`` / ``zero_v`` pack zeros in place of the N(0, 1) K / V (the same addresses and work)."""
+    """Paged FP8 attention: Q [4680, 12, 128] over `chunks` chunks (4680 keys each) of FP8 pages.  ``form``:
+    "bf16" the exact form, "qk8" e4m3 queries against the K codes on the fp8 matrix cores, "qkpv8" that and
+    e4m3 weights against the V codes.  ``zero_k`` / ``zero_v`` pack zeros in place of the N(0, 1) K / V (the
+    same addresses and work)."""
     from waveforcing_amd.backend import attn_paged_fp8
     from waveforcing_amd.kv import PagedKV
 
@@ -247,30 +251,31 @@ def bench_attention(steps: int, warmup: int, dev: str, chunks: int = 8, quantize
     q = torch.randn((TOKENS, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
     ctx = PagedKV(pool, table, n_kv)
     out = torch.empty_like(q)
-    ms = _timed(lambda: attn_paged_fp8(q, ctx, out=out, quantized_qk=quantized_qk), steps, warmup, warm_s)
+    kw = ATTN_FORMS[form]
+    ms = _timed(lambda: attn_paged_fp8(q, ctx, out=out, **kw), steps, warmup, warm_s)
     flops = 4.0 * TOKENS * n_kv * H * HEAD_DIM
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops, "keys": n_kv}
 
 
 def bench_attention_data(steps: int, warmup: int, dev: str, repeats: int = 2):
-    """Both attention forms on the attention workload with N(0, 1) or zero K / V in the pages, each timed
+    """The three attention forms on the attention workload with N(0, 1) or zero K / V in the pages, each timed
     after a second of sustained launches: the clock under this load depends on the operand values."""
     res = {}
     for rep in range(repeats):
         for name, zk, zv in (("randn", False, False), ("zero", True, True), ("zero_k", True, False),
                              ("zero_v", False, True)):
-            for qk in (False, True):
-                r = bench_attention(steps, warmup, dev, quantized_qk=qk, zero_k=zk, zero_v=zv, warm_s=1.0)
-                res[f"{name}{'_qk8' if qk else ''}_ms_{rep}"] = round(r["ms"], 4)
+            for form in ATTN_FORMS:
+                r = bench_attention(steps, warmup, dev, form=form, zero_k=zk, zero_v=zv, warm_s=1.0)
+                res[f"{name}{'' if form == 'bf16' else '_' + form}_ms_{rep}"] = round(r["ms"], 4)
     return res
 
 
-def bench_block(scale: str, steps: int, warmup: int, dev: str, quantized_qk: bool = False):
+def bench_block(scale: str, steps: int, warmup: int, dev: str, form: str = "bf16"):
     """One quantized DiT block over one 3-frame chunk (4680 tokens, 30x52 latent grid) with 7 prior
-    chunks of FP8 paged context (37440 keys incl. its own) and a 512-token text context (with
-    ``quantized_qk``, the self-attention through the hip_fp8_qk backend)."""
+    chunks of FP8 paged context (37440 keys incl. its own) and a 512-token text context; ``form`` selects
+    the self-attention backend (bf16: hip_fp8, qk8: hip_fp8_qk, qkpv8: hip_fp8_qkpv)."""
     from waveforcing_amd import rope
-    from waveforcing_amd.backend import _WAVE_STATE, enable_hip_fp8, enable_hip_fp8_qk
+    from waveforcing_amd.backend import _WAVE_STATE, enable_hip_fp8, enable_hip_fp8_qk, enable_hip_fp8_qkpv
     from waveforcing_amd.block import PRESETS, QuantizedWanBlock, random_block_params
 
     cfg = PRESETS[scale]
@@ -300,7 +305,7 @@ def bench_block(scale: str, steps: int, warmup: int, dev: str, quantized_qk: boo
 
     saved = dict(_WAVE_STATE)
     try:
-        (enable_hip_fp8_qk if quantized_qk else enable_hip_fp8)()
+        {"bf16": enable_hip_fp8, "qk8": enable_hip_fp8_qk, "qkpv8": enable_hip_fp8_qkpv}[form]()
         ms = _timed(step, steps, warmup)
     finally:
         _WAVE_STATE.clear()
@@ -664,7 +669,8 @@ def main() -> None:
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
                                        "tick_1p3b", "generate_1p3b", "copy", "attention_qk8", "block_1p3b_qk8",
-                                       "kv_pertensor", "attention_data", "gemm_data"],
+                                       "attention_qkpv8", "block_1p3b_qkpv8", "kv_pertensor", "attention_data",
+                                       "gemm_data"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -685,8 +691,10 @@ def main() -> None:
               "stack_1p3b": bench_stack, "stack_14b": lambda s, w, d: bench_stack(s, w, d, "14b"),
               "dit_1p3b": bench_dit, "tick_1p3b": lambda s, w, d: bench_stack(s, w, d, ticks_only=True),
               "generate_1p3b": bench_generate,
-              "attention_qk8": lambda s, w, d: bench_attention(s, w, d, quantized_qk=True),
-              "block_1p3b_qk8": lambda s, w, d: bench_block("1.3b", s, w, d, quantized_qk=True),
+              "attention_qk8": lambda s, w, d: bench_attention(s, w, d, form="qk8"),
+              "block_1p3b_qk8": lambda s, w, d: bench_block("1.3b", s, w, d, form="qk8"),
+              "attention_qkpv8": lambda s, w, d: bench_attention(s, w, d, form="qkpv8"),
+              "block_1p3b_qkpv8": lambda s, w, d: bench_block("1.3b", s, w, d, form="qkpv8"),
               "kv_pertensor": bench_kv_pertensor, "attention_data": bench_attention_data,
               "gemm_data": bench_gemm_data,
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
@@ -697,10 +705,12 @@ def main() -> None:
     lin = bench_block_linears(max(5, args.steps // 5), 2, dev)
     at_sweep = {c: bench_attention(max(5, args.steps // 5), 2, dev, chunks=c) for c in (1, 2, 4, 8)}
     at = at_sweep[8]
-    at_qk = bench_attention(max(5, args.steps // 5), 2, dev, quantized_qk=True)
+    at_qk = bench_attention(max(5, args.steps // 5), 2, dev, form="qk8")
+    at_pv = bench_attention(max(5, args.steps // 5), 2, dev, form="qkpv8")
     kvt = bench_kv_pertensor(max(5, args.steps // 5), 2, dev)
     b13 = bench_block("1.3b", max(5, args.steps // 5), 2, dev)
-    b13q = bench_block("1.3b", max(5, args.steps // 5), 2, dev, quantized_qk=True)
+    b13q = bench_block("1.3b", max(5, args.steps // 5), 2, dev, form="qk8")
+    b13p = bench_block("1.3b", max(5, args.steps // 5), 2, dev, form="qkpv8")
     b14 = bench_block("14b", max(3, args.steps // 10), 1, dev)
     xch = bench_exchange(max(5, args.steps // 5), 2, dev)
     stk = bench_stack(max(3, args.steps // 10), 1, dev)
@@ -777,6 +787,12 @@ def main() -> None:
             "attn_qk8_note": "the quantized-QK backend (hip_fp8_qk, the SageAttention counterpart): per-query e4m3 "
                              "Q against the pages' K codes on the fp8 matrix cores, exact V; same workload",
             "dit_block_1p3b_qk8_ms_per_chunk": round(b13q["ms"], 4),
+            "attn_paged_fp8_qkpv8_ms": round(at_pv["ms"], 4),
+            "attn_paged_fp8_qkpv8_tflops": round(at_pv["tflops"], 1),
+            "attn_qkpv8_note": "the fp8-PV backend (hip_fp8_qkpv, the form of Sage's fp8 P.V kernels): the "
+                               "quantized-QK form with e4m3 weights p s_v (a power-of-two scale per query and "
+                               "64-key tile) against the pages' V codes on the fp8 matrix cores; same workload",
+            "dit_block_1p3b_qkpv8_ms_per_chunk": round(b13p["ms"], 4),
             "fp8_kv_pertensor_layer_us": round(kvt["us_round_trip"], 2),
             "fp8_kv_pertensor_gbs": round(kvt["gbs"], 1),
             "fp8_kv_pertensor_note": "the reference's per-tensor FP8 KV mode (_all_gather_fp8) on one layer's "
@@ -827,8 +843,8 @@ def main() -> None:
                                                 "second of sustained launches: the clock under the power limit "
                                                 "depends on the operands' switching"},
             "attn_power": {**{k.replace("_ms_0", "_ms"): v for k, v in adat.items()},
-                           "note": "both attention forms on the attention workload with N(0,1) or zero K / V in the "
-                                   "pages, each after a second of sustained launches"},
+                           "note": "the three attention forms on the attention workload with N(0,1) or zero K / V "
+                                   "in the pages, each after a second of sustained launches"},
         },
     }
     print(json.dumps(line), flush=True)

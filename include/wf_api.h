@@ -315,11 +315,11 @@ int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads,
 /* The quantized-QK form of wf_attn_paged_fp8, same arguments: the
  * counterpart of the reference's SageAttention backend (enable_sage /
  * sageattn, wave_rt/runtime/backend.py:57-62,144-146), which quantizes Q and
- * K before QK^T.  Each query row (per head) is quantized to e4m3 with its
- * own scale s_q = amax|q| / 448; scores are sum_d code_q * code_k from the
- * fp8 matrix cores (fp32 accumulation) times s_k * s_q; V and the softmax are
- * exact as in wf_attn_paged_fp8.  Approximate by design (e4m3 queries carry
- * 3 mantissa bits). */
+ * K before QK^T.  Each query row (per head) is quantized to e4m3 with a
+ * power-of-two scale s_q, the smallest with amax|q| <= 448 s_q; scores are
+ * sum_d code_q * code_k from the fp8 matrix cores (fp32 accumulation) times
+ * s_k * s_q; V and the softmax are exact as in wf_attn_paged_fp8.
+ * Approximate by design (e4m3 queries carry 3 mantissa bits). */
 int wf_attn_paged_fp8_qk8(const void* q, int64_t lq, int32_t n_heads,
                           int32_t head_dim, int64_t ldq,
                           const uint8_t* k_codes, const uint8_t* v_codes,
@@ -328,6 +328,24 @@ int wf_attn_paged_fp8_qk8(const void* q, int64_t lq, int32_t n_heads,
                           const int32_t* page_table, int64_t n_table,
                           int64_t n_kv, float softmax_scale, void* out,
                           int64_t ldo, void* stream);
+
+/* wf_attn_paged_fp8_qk8 with the P.V product on the fp8 matrix cores as
+ * well, same arguments: the counterpart of the fp8 P.V product of the
+ * reference's SageAttention backend (sageattn, wave_rt/runtime/backend.py:
+ * 57-62,144-146).  V stays as the pages' e4m3 codes; each query's weights
+ * p_k * s_v,k of a 64-key tile are rounded to e4m3 after division by a
+ * power of two 2^E (the smallest with their maximum <= 448 * 2^E), which
+ * the matrix cores multiply back; the row sum is the fp32 sum of the
+ * unrounded p_k.  Approximate by design: each weight carries 3 mantissa
+ * bits. */
+int wf_attn_paged_fp8_qkpv8(const void* q, int64_t lq, int32_t n_heads,
+                            int32_t head_dim, int64_t ldq,
+                            const uint8_t* k_codes, const uint8_t* v_codes,
+                            const float* k_scales, const float* v_scales,
+                            int64_t pool_pages, int32_t page_tokens,
+                            const int32_t* page_table, int64_t n_table,
+                            int64_t n_kv, float softmax_scale, void* out,
+                            int64_t ldo, void* stream);
 
 /* Attention of q [lq][n_heads][128] over dense bf16 K, V [n_kv][n_heads][128]
  * (token stride ldkv elements), same math and output as wf_attn_paged_fp8

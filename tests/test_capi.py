@@ -102,3 +102,9 @@ def test_pertensor_dequant_and_qk8_argument_errors():
         _lib.call("wf_fp8_dequant_pertensor_f32", 17, 32, 64, 48, None)
     with pytest.raises(RuntimeError, match="head_dim=64"):
         _lib.call("wf_attn_paged_fp8_qk8", 16, 4, 2, 64, 128, 32, 48, 64, 80, 4, 64, 96, 1, 64, 0.1, 112, 128, None)
+    with pytest.raises(RuntimeError, match="wf_attn_paged_fp8_qkpv8: head_dim=64"):
+        _lib.call("wf_attn_paged_fp8_qkpv8", 16, 4, 2, 64, 128, 32, 48, 64, 80, 4, 64, 96, 1, 64, 0.1, 112, 128,
+                  None)
+    with pytest.raises(RuntimeError, match="page_tokens=32 must be >= 64"):
+        _lib.call("wf_attn_paged_fp8_qkpv8", 16, 4, 2, 128, 256, 32, 48, 64, 80, 4, 32, 96, 4, 64, 0.1, 112, 256,
+                  None)

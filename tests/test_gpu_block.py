@@ -34,7 +34,7 @@ from oracle import attention as oat
 from oracle import block as ob
 from oracle import kv as okv
 from waveforcing_amd import rope
-from waveforcing_amd.backend import _WAVE_STATE, enable_hip_fp8, enable_hip_fp8_qk
+from waveforcing_amd.backend import _WAVE_STATE, enable_hip_fp8, enable_hip_fp8_qk, enable_hip_fp8_qkpv
 from waveforcing_amd.block import QuantizedWanBlock, random_block_params
 from waveforcing_amd.kv import Fp8PagePool
 
@@ -64,10 +64,15 @@ def _case(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed):
                 P=P, prior_ids=prior_ids, own_ids=own_ids, ctx_ids=ctx_ids, n_ctx=n_ctx, start_frame=start_frame)
 
 
-def _compare(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed, quantized_qk=False):
+# attention forms: the backend that selects each and the oracle attention of the same form
+_FORMS = {"exact": (enable_hip_fp8, None), "qk8": (enable_hip_fp8_qk, oat.paged_fp8_qk8),
+          "qkpv8": (enable_hip_fp8_qkpv, oat.paged_fp8_qkpv8)}
+
+
+def _compare(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed, form="exact"):
     c = _case(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed)
     print(f"\n[case] dim {dim} heads {heads} ffn {ffn} tokens {c['T']} context {c['n_ctx']} text {text_len}"
-          f"{' quantized QK' if quantized_qk else ''}", flush=True)
+          f" attention {form}", flush=True)
     # GPU
     blk = QuantizedWanBlock(c["params"], heads, DEV)
     pool = Fp8PagePool(c["P"], heads, 128, c["page"], DEV)
@@ -77,7 +82,7 @@ def _compare(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed, quanti
     x_gpu = c["x"].to(DEV).clone()
     saved = dict(_WAVE_STATE)
     try:
-        (enable_hip_fp8_qk if quantized_qk else enable_hip_fp8)()
+        _FORMS[form][0]()
         blk.forward(x_gpu, c["e"].to(DEV), cos, sin, pool, pool.page_table(c["ctx_ids"]),
                     pool.page_table(c["own_ids"]), c["n_ctx"], (tk, tv))
     finally:
@@ -96,7 +101,7 @@ def _compare(dim, heads, ffn, frames, h, w, prior_chunks, text_len, seed, quanti
     tk_err = (tk.cpu().double() - otk.double()).abs().max().item()
     ref = ob.block_forward(c["params"], c["x"], c["e"], (frames, h, w), c["start_frame"], pk, pv, c["ctx_ids"],
                            c["own_ids"], c["n_ctx"], c["page"], otk, otv, heads,
-                           paged_attn=oat.paged_fp8_qk8 if quantized_qk else None).double()
+                           paged_attn=_FORMS[form][1]).double()
     codes_same = (own_k == pk[0][c["own_ids"]]).double().mean().item()
     rel = ((out - ref).norm() / ref.norm()).item()
     mx = (out - ref).abs().max().item()
@@ -121,7 +126,14 @@ def test_block_14b_whole_chunk_matches_oracle():
 def test_block_1p3b_whole_chunk_quantized_qk_matches_oracle():
     """The block through the hip_fp8_qk backend (the counterpart of the reference's Sage path) against the
     oracle block with the quantized-QK attention, same bar."""
-    _compare(1536, 12, 8960, 3, 30, 52, prior_chunks=7, text_len=512, seed=8, quantized_qk=True)
+    _compare(1536, 12, 8960, 3, 30, 52, prior_chunks=7, text_len=512, seed=8, form="qk8")
+
+
+def test_block_1p3b_whole_chunk_fp8_pv_matches_oracle():
+    """The block through the hip_fp8_qkpv backend (both attention products on e4m3 operands, the form of Sage's
+    fp8 P.V kernels) against the oracle block with the same attention form, same bar; 3 prior chunks (18720
+    context keys) keep the oracle's tile-by-tile attention short."""
+    _compare(1536, 12, 8960, 3, 30, 52, prior_chunks=3, text_len=512, seed=9, form="qkpv8")
 
 
 @pytest.mark.parametrize("kind", ["residuals", "attn_mod", "cross", "ffn_mod", "self_qk", "cross_q"])

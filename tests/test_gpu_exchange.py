@@ -16,7 +16,9 @@ rotation at ``csf - wflen - npb``.  Checked for every (pass, layer):
   bit for bit, the dequantized pages the closure hands to attention;
 * the attention output equals the oracle's fp32 SDPA over that context within
   2e-2 max-abs (with the ``hip_fp8_qk`` backend, the oracle's quantized-QK
-  attention over the context's codes, same bar);
+  attention over the context's codes, with ``hip_fp8_qkpv`` the oracle's
+  fp8-PV attention over the K and V codes, beyond its rounding margin for
+  weights within 2^-15 of an e4m3 rounding midpoint; same bar);
 * ``prof_read()`` reports the context length as ``klen`` and positive
   exchange and attention times.
 
@@ -74,11 +76,12 @@ def _model_context(clean, live, inflight, plan, rank, layer, raw=False):
     return rt(torch.cat(ks, 0)), rt(torch.cat(vs, 0))
 
 
-@pytest.mark.parametrize("attn", ["hip_fp8", "hip_fp8_qk"])
+@pytest.mark.parametrize("attn", ["hip_fp8", "hip_fp8_qk", "hip_fp8_qkpv"])
 def test_wavefront_contexts_and_patched_attention_match_list_model(attn):
     x = ex.PagedExchange(n_layers=LAYERS, n_heads=H, tokens_per_frame=HT * WD, frames_per_chunk=NPB,
                          max_attn_frames=WINDOW, rf_step=RF, device=DEV)
-    (backend.enable_hip_fp8 if attn == "hip_fp8" else backend.enable_hip_fp8_qk)()
+    {"hip_fp8": backend.enable_hip_fp8, "hip_fp8_qk": backend.enable_hip_fp8_qk,
+     "hip_fp8_qkpv": backend.enable_hip_fp8_qkpv}[attn]()
     clean = []
     longest = 0
     try:
@@ -120,12 +123,13 @@ def test_wavefront_contexts_and_patched_attention_match_list_model(attn):
                     assert torch.equal(k.cpu(), wk) and torch.equal(vv.cpu(), wv), f"tick {t} rank {rank} L{layer}"
                     assert attn_ms > 0 and exch_ms > 0
                     if attn == "hip_fp8":
-                        ref = oat.sdpa(q[0], wk, wv)
+                        ref, margin = oat.sdpa(q[0], wk, wv), 0.0
                     else:
-                        kc, ksc = okv.quantize_rows(_model_context(clean, live, inflight, plan, rank, layer,
-                                                                   raw=True)[0])
-                        ref = oat.sdpa_qk8(q[0], kc, ksc, wv)
-                    err = (out[0].cpu().float() - ref).abs().max().item()
+                        rk, rv = _model_context(clean, live, inflight, plan, rank, layer, raw=True)
+                        kc, ksc = okv.quantize_rows(rk)
+                        ref, margin = (oat.sdpa_qk8(q[0], kc, ksc, wv), 0.0) if attn == "hip_fp8_qk" else \
+                            oat.sdpa_qkpv8(q[0], kc, ksc, *okv.quantize_rows(rv), margin_eps=2.0 ** -15)
+                    err = ((out[0].cpu().float() - ref).abs() - margin).max().item()
                     assert out.shape == q.shape and err <= 2e-2, f"tick {t} rank {rank} L{layer}: {err:.3e}"
                     longest = max(longest, wk.shape[0])
             backend.set_exchange_fn(None)

@@ -144,3 +144,79 @@ def test_qk8_closed_forms_and_error_scale():
     exact = oat.paged_fp8(q, kp, vp, ids, 200, 64)
     err = (got - exact).abs().max().item()
     assert 0 < err < 2e-2
+
+
+# ---- the fp8-PV form (oracle.attention.sdpa_qkpv8) ----------------------------------------------------------------
+
+def _codes_and_scales(x):
+    return okv.quantize_rows(x)
+
+
+def _exact_v(vc, vs):
+    return vc.view(okv.FP8).float() * vs[..., None]
+
+
+def test_qkpv8_without_weight_rounding_is_the_quantized_qk_form():
+    """With the weights left unrounded the tile-by-tile evaluation (lazy maxima shared by groups of 32 queries,
+    rescaled sums, masked tail keys) must give the quantized-QK attention of the definition over V = code * s.
+    Later tiles carry keys scaled up 3x per tile, so the running maxima move by far more than the rescale
+    threshold and the rescale path runs."""
+    for Lq, H, n, seed in ((70, 2, 200, 0), (33, 1, 64, 1), (5, 1, 65, 2), (100, 2, 1, 3), (40, 1, 300, 4)):
+        q, k, v = _rand((Lq, H, 128), seed), _rand((n, H, 128), seed + 10), _rand((n, H, 128), seed + 20)
+        if seed == 4:
+            grow = torch.pow(3.0, (torch.arange(n) // 64).float())[:, None, None]
+            k = (k.float() * grow).to(torch.bfloat16)
+        kc, ks = _codes_and_scales(k)
+        vc, vs = _codes_and_scales(v)
+        got = oat.sdpa_qkpv8(q, kc, ks, vc, vs, round_p=False)
+        want = oat.sdpa_qk8(q, kc, ks, _exact_v(vc, vs))
+        assert (got - want).abs().max().item() < 1e-4, (Lq, H, n)    # fp32 exponents against float64 ones
+        rounded = oat.sdpa_qkpv8(q, kc, ks, vc, vs)
+        assert 0 < (rounded - want).abs().max().item() < 0.2
+
+
+def _round4(x: float) -> float:
+    """x > 0 to 4 significant bits, ties to even (e4m3's normal precision)."""
+    m, e = math.frexp(x)
+    r = m * 16.0
+    n = math.floor(r)
+    if r - n > 0.5 or (r - n == 0.5 and n % 2 == 1):
+        n += 1
+    return math.ldexp(n / 16.0, e)
+
+
+def test_qkpv8_single_key_carries_its_scale_with_four_significant_bits():
+    """Zero queries over one key: p = 1, the weight is s_v itself, rounded to 4 significant bits (ties to even):
+    out = round4(s_v) * code_v.  Scales with significands 1, 1.0625 (a tie, to 1), 1.09375 (to 1.125),
+    1.75, 1.875 and 1.9921875 (to 2) at several powers of two."""
+    for f in (1.0, 1.0625, 1.09375, 1.75, 1.875, 1.9921875):
+        for j in (-12, -7, 0, 3):
+            v = _rand((1, 1, 128), 30) * 0.01
+            v[0, 0, 7] = 448.0 * f * 2.0 ** j
+            vc, vs = _codes_and_scales(v)
+            assert float(vs[0, 0]) == f * 2.0 ** j
+            kc, ks = _codes_and_scales(_rand((1, 1, 128), 31))
+            got = oat.sdpa_qkpv8(torch.zeros((3, 1, 128), dtype=torch.bfloat16), kc, ks, vc, vs)
+            want = vc[0, 0].view(okv.FP8).float() * _round4(f * 2.0 ** j)
+            assert torch.equal(got[:, 0], want[None].expand(3, 128)), (f, j)
+
+
+def test_qkpv8_equal_scores_with_power_of_two_scales_give_the_mean_of_v():
+    g = torch.Generator().manual_seed(32)
+    n = 300
+    codes = torch.randint(0, 126, (n, 2, 128), generator=g, dtype=torch.uint8)
+    codes[:, :, 0] = 126
+    vals = codes.view(okv.FP8).float() * torch.where(torch.rand((n, 2, 128), generator=g) < 0.5, -1.0, 1.0)
+    v = (vals * torch.pow(2.0, torch.randint(-9, 0, (n, 2, 1), generator=g).float())).to(torch.bfloat16)
+    vc, vs = _codes_and_scales(v)
+    kc, ks = _codes_and_scales(_rand((n, 2, 128), 33))
+    got = oat.sdpa_qkpv8(torch.zeros((5, 2, 128), dtype=torch.bfloat16), kc, ks, vc, vs)
+    want = v.double().mean(0)
+    assert (got.double() - want[None]).abs().max().item() < 1e-6
+
+
+def test_pv8_exponent_rule():
+    mx = torch.tensor([448.0, 448.5, 224.0, 224.5, 256.0, 1.0, 0.0, 2.0 ** -200, 1e38], dtype=torch.float64)
+    assert oat.pv8_exponent(mx).tolist() == [0, 1, -1, 0, 0, -8, 0, -126, 118]
+    e = oat.pv8_exponent(mx[:6]).double()
+    assert ((mx[:6] <= 448 * torch.pow(2.0, e)) & (mx[:6] > 448 * torch.pow(2.0, e - 1))).all()

@@ -99,6 +99,10 @@ SIGNATURES: dict[str, list] = {
         _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _i64, _i32, _c_void_p, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p,
     ],
+    "wf_attn_paged_fp8_qkpv8": [
+        _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _i64, _i32, _c_void_p, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p,
+    ],
     "wf_attn_dense_bf16": [
         _c_void_p, _i64, _i32, _i32, _i64, _c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p,
     ],

@@ -15,6 +15,8 @@ of the reference's SageAttention backend (``enable_sage``, backend.py:57-62,
 144-146): the same call over the same pages through ``wf_attn_paged_fp8_qk8``,
 which quantizes each query to e4m3 and runs QK^T on the fp8 matrix cores
 against the pages' K codes, with V exact; approximate by design, like Sage.
+``hip_fp8_qkpv`` (``wf_attn_paged_fp8_qkpv8``) also runs P.V on the fp8 matrix
+cores, against the pages' V codes, as Sage's fp8 P.V product does.
 """
 
 from __future__ import annotations
@@ -28,7 +30,7 @@ import torch
 from . import _lib
 from .kv import PagedKV
 
-ATTENTION_BACKENDS = ("torch_sdpa", "fa_custom", "sa", "fa", "fa2", "hip_fp8", "hip_fp8_qk")
+ATTENTION_BACKENDS = ("torch_sdpa", "fa_custom", "sa", "fa", "fa2", "hip_fp8", "hip_fp8_qk", "hip_fp8_qkpv")
 
 _WAVE_STATE: dict = {
     "exchange_fn": None,
@@ -59,13 +61,14 @@ def prof_read() -> tuple:
 
 def attn_paged_fp8(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, causal: bool = False,
                    softmax_scale: float | None = None, out: torch.Tensor | None = None,
-                   quantized_qk: bool = False) -> torch.Tensor:
+                   quantized_qk: bool = False, fp8_pv: bool = False) -> torch.Tensor:
     """flash_attn_func-shaped call: q [1, Lq, H, D] (or [Lq, H, D]) bf16 over a paged FP8 context.
 
     ``k`` carries both pools; ``v`` is accepted for call compatibility and
     must be ``k`` itself or None.  Returns bf16 with q's shape.  With
     ``quantized_qk`` the scores come from e4m3 queries against the K codes
-    on the fp8 matrix cores (wf_attn_paged_fp8_qk8).
+    on the fp8 matrix cores (wf_attn_paged_fp8_qk8); ``fp8_pv`` (which implies
+    it) runs P.V there too, against the V codes (wf_attn_paged_fp8_qkpv8).
     """
     if causal:
         raise ValueError("the wavefront attention is non-causal over the context (backend.py:141-148)")
@@ -86,8 +89,9 @@ def attn_paged_fp8(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, causal
     o = out if out is not None else torch.empty((Lq, H, D), dtype=torch.bfloat16, device=q3.device)
     if o.dim() == 4:
         o = o[0]
+    entry = "wf_attn_paged_fp8_qkpv8" if fp8_pv else "wf_attn_paged_fp8_qk8" if quantized_qk else "wf_attn_paged_fp8"
     _lib.call(
-        "wf_attn_paged_fp8_qk8" if quantized_qk else "wf_attn_paged_fp8", q3.data_ptr(), Lq, H, D, q3.stride(0),
+        entry, q3.data_ptr(), Lq, H, D, q3.stride(0),
         pool.k_codes.data_ptr(), pool.v_codes.data_ptr(), pool.k_scales.data_ptr(), pool.v_scales.data_ptr(),
         pool.pool_pages, pool.page_tokens, k.table.dev.data_ptr(), len(k.table), k.n_tokens,
         float(softmax_scale), o.data_ptr(), o.stride(0), _lib.stream_handle(q3.device),
@@ -127,6 +131,12 @@ def attn_paged_fp8_qk(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, cau
     return attn_paged_fp8(q, k, v, causal, softmax_scale, out, quantized_qk=True)
 
 
+def attn_paged_fp8_qkpv(q: torch.Tensor, k: PagedKV, v: PagedKV | None = None, causal: bool = False,
+                        softmax_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The quantized-QK form with the fp8 P.V product (the ``fa_func`` of ``hip_fp8_qkpv``)."""
+    return attn_paged_fp8(q, k, v, causal, softmax_scale, out, fp8_pv=True)
+
+
 def enable_hip_fp8() -> None:
     """Use the gfx950 paged-FP8 attention on the wavefront path."""
     _WAVE_STATE["attn"] = "hip_fp8"
@@ -140,16 +150,24 @@ def enable_hip_fp8_qk() -> None:
     _WAVE_STATE["fa_func"] = attn_paged_fp8_qk
 
 
+def enable_hip_fp8_qkpv() -> None:
+    """Use the paged-FP8 attention with both products on the fp8 matrix cores (e4m3 queries against the K
+    codes; e4m3 weights p s_v against the V codes), the form of SageAttention's fp8 P.V kernels."""
+    _WAVE_STATE["attn"] = "hip_fp8_qkpv"
+    _WAVE_STATE["fa_func"] = attn_paged_fp8_qkpv
+
+
 def paged_attention():
-    """The paged attention the blocks run: the quantized-QK form when ``hip_fp8_qk`` is selected, the exact
-    form otherwise."""
-    return attn_paged_fp8_qk if _WAVE_STATE["attn"] == "hip_fp8_qk" else attn_paged_fp8
+    """The paged attention the blocks run: the quantized form that ``hip_fp8_qk`` or ``hip_fp8_qkpv`` selects,
+    the exact form otherwise."""
+    return {"hip_fp8_qk": attn_paged_fp8_qk, "hip_fp8_qkpv": attn_paged_fp8_qkpv}.get(_WAVE_STATE["attn"],
+                                                                                    attn_paged_fp8)
 
 
 def attend(roped_query, ctx_k, ctx_v, sdpa: Callable | None = None):
     """Attention dispatch of the patched forward (backend.py:141-148)."""
     attn = _WAVE_STATE["attn"]
-    if attn in ("hip_fp8", "hip_fp8_qk"):
+    if attn in ("hip_fp8", "hip_fp8_qk", "hip_fp8_qkpv"):
         return _WAVE_STATE["fa_func"](roped_query, ctx_k, ctx_v, causal=False)
     if attn == "fa_custom":
         return _WAVE_STATE["fa_func"](roped_query, ctx_k, ctx_v, causal=False)
@@ -187,3 +205,4 @@ def exchange_and_attend(layer_idx: int, roped_query, roped_key, unroped_key, val
         ev.record()
         sink.append(ev)
     return out
+

@@ -64,6 +64,8 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef short v2s16 __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 
@@ -86,6 +88,11 @@ constexpr int KP8 = D + 16;
 constexpr int K8_TILE = BKV * KP8;
 constexpr int KS_BYTES = BKV * 4;
 constexpr int STAGE8 = K8_TILE + V_TILE + KS_BYTES;
+// The fp8-PV form keeps V as codes too: [key][d] rows of 128 codes whose four 32-byte d blocks are permuted per
+// key (block db of key k at position db ^ sig(k), sig(k) = bit 1 of k | bit 3 of k << 1), so the transposing
+// 8-byte reads of a half-wave (8 keys x 32 bytes) fall on 64 distinct banks; after V the tile's u_k and V scales.
+constexpr int V8_TILE = BKV * D;
+constexpr int STAGE_PV8 = K8_TILE + V8_TILE + 2 * KS_BYTES;
 constexpr int OPITCH = D * 2 + 8;       // staged output row pitch (bytes)
 constexpr int OUT_STAGING = WAVES * 32 * OPITCH;
 constexpr int kBufferRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
@@ -139,6 +146,13 @@ __device__ inline v4s read_tr(const uint8_t* addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(addr));
 }
 
+// 8 bytes of an 8-bit transposing LDS read (ds_read_b64_tr_b8): within each 16-lane group, lane i receives
+// byte i % 8 of the 8-byte chunks addressed by lanes 2 j + i / 8 as its bytes j = 0..7.
+__device__ inline v2i read_tr8(const uint8_t* addr) {
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(addr));
+}
+
 // max / sum of v over lanes l and l ^ 32 (v_permlane32_swap): a lane's two
 // halves of a score column.  The swap is inline asm: the ROCm 7.2 compiler
 // reads both results of __builtin_amdgcn_permlane32_swap from the
@@ -167,12 +181,20 @@ __device__ inline float pair_sum(float v) {
 // staging stores u_k = s_k * softmax scale * log2(e) per key, the same for every query, so a score's exponent
 // is one FMA, s'' u_k - m; the tile's maximum is bounded by max s'' * max u_k (exact maxima only in the rare
 // rescale).  V and P stay exact as in the bf16 form.
-template <bool DENSE, bool QK8>
+//
+// PV8 (with QK8): the fp8-PV form, the counterpart of the fp8 P.V product of the reference's SageAttention
+// backend.  V stays as the pages' codes in LDS and O^T += V^T P^T runs on the fp8 matrix cores too: the key
+// scale s_v goes into P, each query's 64 values p_k s_v,k of a tile are rounded to e4m3 after division by
+// 2^E, the smallest power of two that brings their maximum to <= 448 (the same rule as the queries'), and 2^E
+// is the MFMA's block scale of that query's column.  The row sum stays the fp32 sum of the unrounded p_k.
+template <bool DENSE, bool QK8, bool PV8>
 __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) {
   static_assert(!(DENSE && QK8), "the quantized-QK form reads FP8 pages");
-  constexpr int kStage = QK8 ? STAGE8 : STAGE;
-  constexpr int kVOff = QK8 ? K8_TILE : K_TILE;  // V rows within a stage
-  constexpr int kSOff = K8_TILE + V_TILE;        // K scales within a stage (QK8)
+  static_assert(!PV8 || QK8, "the fp8-PV form extends the quantized-QK form");
+  constexpr int kStage = PV8 ? STAGE_PV8 : QK8 ? STAGE8 : STAGE;
+  constexpr int kVOff = QK8 ? K8_TILE : K_TILE;              // V rows within a stage
+  constexpr int kSOff = K8_TILE + (PV8 ? V8_TILE : V_TILE);  // u_k within a stage (QK8)
+  constexpr int kVSOff = kSOff + KS_BYTES;                   // V scales within a stage (PV8)
   constexpr int kLds = 2 * kStage > OUT_STAGING ? 2 * kStage : OUT_STAGING;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
 
@@ -307,7 +329,13 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // The staged tile as bf16 [key][d] row pieces (registers only), and their
   // write into LDS stage `buf`.
   auto dequant_tile = [&](uint4* out) {
-    if constexpr (QK8) {
+    if constexpr (PV8) {
+      // K and V codes as they are, u_k and the V scale alongside
+      out[0] = make_uint4(sk0[0], sk0[1], sk0[2], sk0[3]);
+      out[1] = make_uint4(__builtin_bit_cast(uint32_t, __fmul_rn(ssk, p.qk_scale)), __builtin_bit_cast(uint32_t, ssv),
+                          0u, 0u);
+      out[2] = make_uint4(sv0[0], sv0[1], sv0[2], sv0[3]);
+    } else if constexpr (QK8) {
       // K codes as they are, the key's exponent factor u_k = s_k * softmax scale * log2(e) alongside; V as in
       // the bf16 form
       out[0] = make_uint4(sk0[0], sk0[1], sk0[2], sk0[3]);
@@ -333,6 +361,15 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
     }
   };
   auto write_tile = [&](int buf, const uint4* v) {
+    if constexpr (PV8) {
+      uint8_t* sb = lds + buf * kStage;
+      *reinterpret_cast<uint4*>(sb + skey * KP8 + schunk * 16) = v[0];
+      if (schunk == 0) *reinterpret_cast<uint32_t*>(sb + kSOff + skey * 4) = v[1].x;
+      if (schunk == 1) *reinterpret_cast<uint32_t*>(sb + kVSOff + skey * 4) = v[1].y;
+      const int sig = ((skey >> 1) & 1) | ((skey >> 2) & 2);
+      *reinterpret_cast<uint4*>(sb + kVOff + skey * D + (((schunk >> 1) ^ sig) << 5) + 16 * (schunk & 1)) = v[2];
+      return;
+    }
     uint4* dv = reinterpret_cast<uint4*>(lds + buf * kStage + kVOff + skey * VP + schunk * 32);
     if constexpr (QK8) {
       *reinterpret_cast<uint4*>(lds + buf * kStage + skey * KP8 + schunk * 16) = v[0];
@@ -423,6 +460,19 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
   // 16t + 8r + 4 half + j, the key order of its P registers.
   const int k_lane = QK8 ? l32 * KP8 + half * 32 : l32 * KP + half * 16;
   const int v_lane = kVOff + (4 * half + ((lane & 15) >> 2)) * VP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
+  // PV8: the V^T operand of d block db gives lane (m, half) d = 32 db + m at 32 keys, its bytes 8 r + j (read r
+  // = 0..3) for key 16 r + 8 (j / 4) + 4 half + j % 4, which is the key of P byte 8 r + j (P bytes 16 b + i are
+  // the score registers s[b][i]).  Lane s of a 16-lane group therefore addresses key 16 r + key0 with
+  // j = s / 2, at d = 32 db + 16 (group % 2) + 8 (s % 2), in the key's permuted d block.
+  int v8_off[4];
+  if constexpr (PV8) {
+    const int jj = (lane & 15) >> 1;
+    const int key0 = 8 * (jj >> 2) + 4 * half + (jj & 3);
+    const int sig = ((jj >> 1) & 1) | ((jj >> 2) << 1);  // sig(16 r + key0)
+    const int o8 = 16 * ((lane >> 4) & 1) + 8 * (lane & 1);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) v8_off[db] = kVOff + key0 * D + ((db ^ sig) << 5) + o8;
+  }
 
   v16f o[4];
 #pragma unroll
@@ -512,16 +562,32 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
     // during the softmax).
     write_tile(cur ^ 1, nxt);
     load_tile((it + 2) * BKV, cur_next);
-    v8bf vf[4][4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
+    v8bf vf[PV8 ? 1 : 4][4];
+    v8i vf8[4];
+    float4 svv[2][4];  // PV8: s_v of the lane's keys 32 b + 8 g + 4 half + 0..3
+    if constexpr (PV8) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const uint8_t* va = st + v_lane + (16 * t) * VP + db * 64;
-        const v4s lo = read_tr(va);
-        const v4s hi = read_tr(va + 8 * VP);
-        vf[t][db] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        const uint8_t* va = st + v8_off[db];
+        const v2i r0 = read_tr8(va), r1 = read_tr8(va + 16 * D), r2 = read_tr8(va + 32 * D), r3 = read_tr8(va + 48 * D);
+        vf8[db] = v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
       }
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          svv[b][g] = *reinterpret_cast<const float4*>(st + kVSOff + 4 * (32 * b + 8 * g + 4 * half));
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const uint8_t* va = st + v_lane + (16 * t) * VP + db * 64;
+          const v4s lo = read_tr(va);
+          const v4s hi = read_tr(va + 8 * VP);
+          vf[t][db] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    }
 
     // QK8: u_k of the lane's 32 keys as an array (element 4 g + e of block b), 1 for keys past n_kv (whose
     // scale reads as zero: their masked score of -inf then still yields a zero weight)
@@ -584,6 +650,56 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       m_use = m_new;
       m_thr = m_new + kTau / c;
       neg_mc = (m_new == -INFINITY) ? 0.f : -m_new * c;
+    }
+    if constexpr (PV8) {
+      // p_k (row sum) and p_k s_v,k; their maximum over the query's 64 keys (both halves) sets 2^E; the
+      // e4m3 codes of p_k s_v,k / 2^E are P's bytes (byte 16 b + i = score register s[b][i])
+      float pv[2][16];
+      float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float sv4[4] = {svv[b][g].x, svv[b][g].y, svv[b][g].z, svv[b][g].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float pe = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g + e], u[b][4 * g + e], neg_mc));
+            ls[e] += pe;
+            pv[b][4 * g + e] = pe * sv4[e];
+          }
+        }
+      l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+      float mx = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, pv[b][e]);
+      mx = pair_max(mx);
+      // E: mx = f 2^X with f in [0.5, 1); mx <= 448 2^E from E = X - 9 when f <= 0.875, else X - 8 (E = 0 for
+      // an all-zero P); clamped to [-126, 127], where 2^E is a normal float and 127 + E an E8M0 scale
+      int E = 0;
+      if (mx > 0.f) {
+        const int X = __builtin_amdgcn_frexp_expf(mx);
+        E = __builtin_amdgcn_frexp_mantf(mx) <= 0.875f ? X - 9 : X - 8;
+        E = min(max(E, -126), 127);
+      }
+      const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(127 + E) << 23);  // 2^E
+      int pw[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        const int b = w >> 2, i = 4 * (w & 3);
+        v2s16 t = {0, 0};
+        t = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(t, pv[b][i], pv[b][i + 1], sc, false);
+        t = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(t, pv[b][i + 2], pv[b][i + 3], sc, true);
+        pw[w] = __builtin_bit_cast(int, t);
+      }
+      const v8i pb = {pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        o[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf8[db], pb, o[db], 0, 0, 0, 127, 0, 127 + E);
+      cur_next = cursor_next(cur_next, (it + 3) * BKV);
+      __syncthreads();
+      return;
     }
     // P for 16-key step t (keys 16t..16t+15 of the tile): elements 0-3 are
     // keys 4 half + 0..3, elements 4-7 keys 8 + 4 half + 0..3; each step's
@@ -651,18 +767,22 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
 
 }  // namespace
 
-template <bool DENSE, bool QK8>
+template <bool DENSE, bool QK8, bool PV8>
 int launch_attn(const AttnArgs& p, int64_t lq, int n_heads, hipStream_t stream) {
   const int64_t items = (lq + BQ - 1) / BQ * n_heads;
   const dim3 grid(static_cast<uint32_t>((items + 7) / 8 * 8));
-  hipLaunchKernelGGL((attn_paged_fp8_kernel<DENSE, QK8>), grid, dim3(THREADS), 0, stream, p);
-  return check_launch(DENSE ? "wf_attn_dense_bf16" : QK8 ? "wf_attn_paged_fp8_qk8" : "wf_attn_paged_fp8");
+  hipLaunchKernelGGL((attn_paged_fp8_kernel<DENSE, QK8, PV8>), grid, dim3(THREADS), 0, stream, p);
+  return check_launch(DENSE  ? "wf_attn_dense_bf16"
+                      : PV8 ? "wf_attn_paged_fp8_qkpv8"
+                      : QK8 ? "wf_attn_paged_fp8_qk8"
+                            : "wf_attn_paged_fp8");
 }
 
 }  // namespace wf
 
 namespace {
-int attn_paged_entry(const char* fn, bool qk8, const void* q, int64_t lq, int32_t n_heads, int32_t head_dim,
+// form: 0 the exact bf16 form, 1 quantized QK, 2 quantized QK and fp8 PV
+int attn_paged_entry(const char* fn, int form, const void* q, int64_t lq, int32_t n_heads, int32_t head_dim,
                      int64_t ldq, const uint8_t* k_codes, const uint8_t* v_codes, const float* k_scales,
                      const float* v_scales, int64_t pool_pages, int32_t page_tokens, const int32_t* page_table,
                      int64_t n_table, int64_t n_kv, float softmax_scale, void* out, int64_t ldo, void* stream) {
@@ -707,8 +827,11 @@ int attn_paged_entry(const char* fn, bool qk8, const void* q, int64_t lq, int32_
   p.pool_pages = static_cast<int>(pool_pages);
   p.page_div = wf::FastDiv(static_cast<uint32_t>(page_tokens));
   p.qk_scale = softmax_scale * wf::kLog2e;
-  return qk8 ? wf::launch_attn<false, true>(p, lq, n_heads, wf::as_stream(stream))
-             : wf::launch_attn<false, false>(p, lq, n_heads, wf::as_stream(stream));
+  switch (form) {
+    case 1: return wf::launch_attn<false, true, false>(p, lq, n_heads, wf::as_stream(stream));
+    case 2: return wf::launch_attn<false, true, true>(p, lq, n_heads, wf::as_stream(stream));
+    default: return wf::launch_attn<false, false, false>(p, lq, n_heads, wf::as_stream(stream));
+  }
 }
 }  // namespace
 
@@ -717,7 +840,7 @@ extern "C" int wf_attn_paged_fp8(const void* q, int64_t lq, int32_t n_heads, int
                                  const float* v_scales, int64_t pool_pages, int32_t page_tokens,
                                  const int32_t* page_table, int64_t n_table, int64_t n_kv, float softmax_scale,
                                  void* out, int64_t ldo, void* stream) {
-  return attn_paged_entry("wf_attn_paged_fp8", false, q, lq, n_heads, head_dim, ldq, k_codes, v_codes, k_scales,
+  return attn_paged_entry("wf_attn_paged_fp8", 0, q, lq, n_heads, head_dim, ldq, k_codes, v_codes, k_scales,
                           v_scales, pool_pages, page_tokens, page_table, n_table, n_kv, softmax_scale, out, ldo,
                           stream);
 }
@@ -727,7 +850,17 @@ extern "C" int wf_attn_paged_fp8_qk8(const void* q, int64_t lq, int32_t n_heads,
                                      const float* v_scales, int64_t pool_pages, int32_t page_tokens,
                                      const int32_t* page_table, int64_t n_table, int64_t n_kv, float softmax_scale,
                                      void* out, int64_t ldo, void* stream) {
-  return attn_paged_entry("wf_attn_paged_fp8_qk8", true, q, lq, n_heads, head_dim, ldq, k_codes, v_codes, k_scales,
+  return attn_paged_entry("wf_attn_paged_fp8_qk8", 1, q, lq, n_heads, head_dim, ldq, k_codes, v_codes, k_scales,
+                          v_scales, pool_pages, page_tokens, page_table, n_table, n_kv, softmax_scale, out, ldo,
+                          stream);
+}
+
+extern "C" int wf_attn_paged_fp8_qkpv8(const void* q, int64_t lq, int32_t n_heads, int32_t head_dim, int64_t ldq,
+                                       const uint8_t* k_codes, const uint8_t* v_codes, const float* k_scales,
+                                       const float* v_scales, int64_t pool_pages, int32_t page_tokens,
+                                       const int32_t* page_table, int64_t n_table, int64_t n_kv,
+                                       float softmax_scale, void* out, int64_t ldo, void* stream) {
+  return attn_paged_entry("wf_attn_paged_fp8_qkpv8", 2, q, lq, n_heads, head_dim, ldq, k_codes, v_codes, k_scales,
                           v_scales, pool_pages, page_tokens, page_table, n_table, n_kv, softmax_scale, out, ldo,
                           stream);
 }
@@ -764,5 +897,5 @@ extern "C" int wf_attn_dense_bf16(const void* q, int64_t lq, int32_t n_heads, in
   p.page_tokens = 1;
   p.page_div = wf::FastDiv(1);
   p.qk_scale = softmax_scale * wf::kLog2e;
-  return wf::launch_attn<true, false>(p, lq, n_heads, wf::as_stream(stream));
+  return wf::launch_attn<true, false, false>(p, lq, n_heads, wf::as_stream(stream));
 }
