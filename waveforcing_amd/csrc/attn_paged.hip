@@ -655,7 +655,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       // p_k (row sum) and p_k s_v,k; their maximum over the query's 64 keys (both halves) sets 2^E; the
       // e4m3 codes of p_k s_v,k / 2^E are P's bytes (byte 16 b + i = score register s[b][i])
       float pv[2][16];
-      float ls[4] = {0.f, 0.f, 0.f, 0.f};
+      float ls[4];
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -664,7 +664,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float pe = __builtin_amdgcn_exp2f(fmaf(s[b][4 * g + e], u[b][4 * g + e], neg_mc));
-            ls[e] += pe;
+            ls[e] = (b == 0 && g == 0) ? pe : ls[e] + pe;
             pv[b][4 * g + e] = pe * sv4[e];
           }
         }
@@ -688,7 +688,8 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
 #pragma unroll
       for (int w = 0; w < 8; ++w) {
         const int b = w >> 2, i = 4 * (w & 3);
-        v2s16 t = {0, 0};
+        // the first conversion's untouched high half is any value (here pv's own bits): the second overwrites it
+        v2s16 t = __builtin_bit_cast(v2s16, pv[b][i]);
         t = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(t, pv[b][i], pv[b][i + 1], sc, false);
         t = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(t, pv[b][i + 2], pv[b][i + 3], sc, true);
         pw[w] = __builtin_bit_cast(int, t);
