@@ -440,10 +440,12 @@ def bench_stack(steps: int, warmup: int, dev: str, preset: str = "1.3b", ticks_o
     return out
 
 
-def bench_dit(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
+def bench_dit(steps: int, warmup: int, dev: str, preset: str = "1.3b", form: str = "bf16"):
     """The whole DiT forward of one chunk from its noisy latent [1, 16, 3, 60, 104] to x0 (patch embedding, time
     embedding, the 30 blocks over the paged exchange, head, unpatchify and flow -> x0), as rank 0's pass of the
-    same steady-state tick as bench_stack (37440-key context), at the first DMD timestep."""
+    same steady-state tick as bench_stack (37440-key context), at the first DMD timestep; ``form`` selects the
+    self-attention backend as in bench_block."""
+    from waveforcing_amd.backend import _WAVE_STATE, enable_hip_fp8, enable_hip_fp8_qk, enable_hip_fp8_qkpv
     from waveforcing_amd.dit import QuantizedWanDiT, random_dit_params
     from waveforcing_amd.exchange import TickPlan
     from waveforcing_amd.stack import QuantizedWanStack
@@ -470,7 +472,13 @@ def bench_dit(steps: int, warmup: int, dev: str, preset: str = "1.3b"):
     def step():
         dit.run_pass(noisy, steps_t[0], p0, x0_out=x0)
 
-    ms = _timed(step, steps, warmup)
+    saved = dict(_WAVE_STATE)
+    try:
+        {"bf16": enable_hip_fp8, "qk8": enable_hip_fp8_qk, "qkpv8": enable_hip_fp8_qkpv}[form]()
+        ms = _timed(step, steps, warmup)
+    finally:
+        _WAVE_STATE.clear()
+        _WAVE_STATE.update(saved)
     ex.abort_tick()
     T = frames * (H // 2) * (W // 2)
     out = {"ms": ms, "layers": len(st.blocks), "tokens": T, "latent": [1, 16, frames, H, W],
@@ -669,8 +677,8 @@ def main() -> None:
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
                                        "tick_1p3b", "generate_1p3b", "copy", "attention_qk8", "block_1p3b_qk8",
-                                       "attention_qkpv8", "block_1p3b_qkpv8", "kv_pertensor", "attention_data",
-                                       "gemm_data"],
+                                       "attention_qkpv8", "block_1p3b_qkpv8", "dit_1p3b_qkpv8", "kv_pertensor",
+                                       "attention_data", "gemm_data"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -695,6 +703,7 @@ def main() -> None:
               "block_1p3b_qk8": lambda s, w, d: bench_block("1.3b", s, w, d, form="qk8"),
               "attention_qkpv8": lambda s, w, d: bench_attention(s, w, d, form="qkpv8"),
               "block_1p3b_qkpv8": lambda s, w, d: bench_block("1.3b", s, w, d, form="qkpv8"),
+              "dit_1p3b_qkpv8": lambda s, w, d: bench_dit(s, w, d, form="qkpv8"),
               "kv_pertensor": bench_kv_pertensor, "attention_data": bench_attention_data,
               "gemm_data": bench_gemm_data,
               "cpu_extra": lambda s, w, d: cpu_baseline_extra()}[args.only]
@@ -716,6 +725,7 @@ def main() -> None:
     stk = bench_stack(max(3, args.steps // 10), 1, dev)
     stk14 = bench_stack(3, 1, dev, "14b")
     dit = bench_dit(max(3, args.steps // 10), 1, dev)
+    ditp = bench_dit(max(3, args.steps // 10), 1, dev, form="qkpv8")
     gen = bench_generate(1, 1, dev)
     gdat = bench_gemm_data(max(3, args.steps // 20), 2, dev)
     adat = bench_attention_data(max(5, args.steps // 5), 2, dev, repeats=1)
@@ -823,6 +833,8 @@ def main() -> None:
                               "the GPU",
             "dit_forward_1p3b_ms_per_chunk": round(dit["ms"], 3),
             "dit_forward_1p3b_tokens_per_s": round(dit["tokens_per_s"], 1),
+            "dit_forward_1p3b_qkpv8_ms_per_chunk": round(ditp["ms"], 3),
+            "dit_forward_1p3b_qkpv8_tokens_per_s": round(ditp["tokens_per_s"], 1),
             "dit_forward_note": "the whole Wan-1.3B DiT forward of one chunk, noisy latent [1,16,3,60,104] -> x0 "
                                 "(patch embedding, time embedding, 30 blocks, head, unpatchify, flow -> x0) as rank "
                                 "0's pass of the same steady-state tick (37440-key context), timestep 1000",
