@@ -15,7 +15,9 @@ cores: 16 v_mfma_i32_32x32x32_i8 of 32 cycles for each of the SIMD's two
 waves) and the epilogue, with the launch's event time and the shader clock (a workgroup's
 cycles over its reference-clock time, averaged).
 With --zero-a the activations are all zero: the same instructions, addresses and bytes, fewer
-toggling bits, so the cycle counts stay and only the clock under the power limit moves.  Stamps are compared
+toggling bits, so the cycle counts stay and only the clock under the power limit moves.  With --fp8 the
+per-tensor e4m3 GEMM (wf_gemm_fp8_pertensor: the same kernel with v_mfma_f32_32x32x64_f8f6f4, 8 MFMAs of
+64 cycles per wave and K step) runs on uniformly random e4m3 codes instead.  Stamps are compared
 only within a workgroup: the shader-clock counters of different XCDs are not
 one time base.
 """
@@ -42,16 +44,24 @@ def _lib(path: str | None = None):
     lib = ctypes.CDLL(path or variant_path("gemm_phases"))
     vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
     lib.wf_gemm_i8.argtypes = [vp, vp, i64, i64, i64, vp, vp, vp, vp, i64, vp, i32, vp]
+    lib.wf_gemm_fp8_pertensor.argtypes = [vp, vp, i64, i64, i64, vp, vp, vp, vp, i64, vp]
     lib.wf_gemm_set_phase_buffer.argtypes = [vp]
     return lib
 
 
-def measure(lib, M: int, N: int, K: int, reps: int, dev="cuda:0", zero_a: bool = False) -> dict:
+def measure(lib, M: int, N: int, K: int, reps: int, dev="cuda:0", zero_a: bool = False, fp8: bool = False) -> dict:
     g = torch.Generator(device=dev).manual_seed(M + N + K)
-    qx = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    if fp8:
+        # uniformly random e4m3 codes, NaN codes (0x7f, 0xff) replaced by 0x7e / 0xfe
+        qx = torch.randint(0, 256, (M, K), generator=g, device=dev, dtype=torch.int32)
+        qw = torch.randint(0, 256, (N, K), generator=g, device=dev, dtype=torch.int32)
+        qx = torch.where((qx & 0x7f) == 0x7f, qx - 1, qx).to(torch.uint8)
+        qw = torch.where((qw & 0x7f) == 0x7f, qw - 1, qw).to(torch.uint8)
+    else:
+        qx = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+        qw = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
     if zero_a:
         qx.zero_()
-    qw = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
     sx = torch.rand((M,), generator=g, device=dev) * 1e-3
     sw = torch.rand((N,), generator=g, device=dev) * 1e-3
     bias = torch.zeros((N,), dtype=torch.bfloat16, device=dev)
@@ -62,10 +72,14 @@ def measure(lib, M: int, N: int, K: int, reps: int, dev="cuda:0", zero_a: bool =
     stream = torch.cuda.current_stream(dev).cuda_stream
 
     def launch():
-        rc = lib.wf_gemm_i8(qx.data_ptr(), qw.data_ptr(), M, N, K, sx.data_ptr(), sw.data_ptr(), bias.data_ptr(),
-                            y.data_ptr(), N, None, 0, stream)
+        if fp8:
+            rc = lib.wf_gemm_fp8_pertensor(qx.data_ptr(), qw.data_ptr(), M, N, K, sx.data_ptr(), sw.data_ptr(),
+                                           bias.data_ptr(), y.data_ptr(), N, stream)
+        else:
+            rc = lib.wf_gemm_i8(qx.data_ptr(), qw.data_ptr(), M, N, K, sx.data_ptr(), sw.data_ptr(), bias.data_ptr(),
+                                y.data_ptr(), N, None, 0, stream)
         if rc != 0:
-            raise RuntimeError(f"wf_gemm_i8 failed with status {rc}")
+            raise RuntimeError(f"GEMM launch failed with status {rc}")
 
     lib.wf_gemm_set_phase_buffer(None)
     t0 = time.perf_counter()
@@ -111,6 +125,7 @@ def main() -> None:
                                                 "gemm_phases variant of this package)")
     ap.add_argument("--shapes", default=None, help="comma-separated indices into the shape list")
     ap.add_argument("--zero-a", action="store_true", help="all-zero activations (same work, fewer toggling bits)")
+    ap.add_argument("--fp8", action="store_true", help="the per-tensor e4m3 GEMM on random e4m3 codes")
     args = ap.parse_args()
     lib = _lib(args.lib)
     shapes = SHAPES if args.shapes is None else [SHAPES[int(i)] for i in args.shapes.split(",")]
@@ -118,7 +133,7 @@ def main() -> None:
           "epilogue (cycles) | event µs | clock (GHz) |")
     print("|---|---|---:|---:|---:|---:|---:|---:|---:|")
     for name, M, N, K in shapes:
-        r = measure(lib, M, N, K, args.reps, zero_a=args.zero_a)
+        r = measure(lib, M, N, K, args.reps, zero_a=args.zero_a, fp8=args.fp8)
         print(f"| {name} | {M} x {N} x {K} | {r['tiles']} | {r['k_steps']} | {r['prologue_cycles']:.0f} | "
               f"{r['cycles_per_k_step']:.0f} | {r['epilogue_cycles']:.0f} | {r['event_us']:.2f} | "
               f"{r['clock_ghz']:.2f} |", flush=True)
