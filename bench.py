@@ -677,7 +677,8 @@ def main() -> None:
     ap.add_argument("--only", choices=["kv", "kv_pack", "kv_unpack", "gemm", "linears_1p3b", "attention", "cpu_extra",
                                        "block_1p3b", "block_14b", "exchange_1p3b", "stack_1p3b", "stack_14b", "dit_1p3b",
                                        "tick_1p3b", "generate_1p3b", "copy", "attention_qk8", "block_1p3b_qk8",
-                                       "attention_qkpv8", "block_1p3b_qkpv8", "dit_1p3b_qkpv8", "kv_pertensor",
+                                       "attention_qkpv8", "block_1p3b_qkpv8", "block_14b_qkpv8", "dit_1p3b_qkpv8",
+                                       "kv_pertensor",
                                        "attention_data", "gemm_data"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
@@ -703,6 +704,7 @@ def main() -> None:
               "block_1p3b_qk8": lambda s, w, d: bench_block("1.3b", s, w, d, form="qk8"),
               "attention_qkpv8": lambda s, w, d: bench_attention(s, w, d, form="qkpv8"),
               "block_1p3b_qkpv8": lambda s, w, d: bench_block("1.3b", s, w, d, form="qkpv8"),
+              "block_14b_qkpv8": lambda s, w, d: bench_block("14b", s, w, d, form="qkpv8"),
               "dit_1p3b_qkpv8": lambda s, w, d: bench_dit(s, w, d, form="qkpv8"),
               "kv_pertensor": bench_kv_pertensor, "attention_data": bench_attention_data,
               "gemm_data": bench_gemm_data,
@@ -721,6 +723,7 @@ def main() -> None:
     b13q = bench_block("1.3b", max(5, args.steps // 5), 2, dev, form="qk8")
     b13p = bench_block("1.3b", max(5, args.steps // 5), 2, dev, form="qkpv8")
     b14 = bench_block("14b", max(3, args.steps // 10), 1, dev)
+    b14p = bench_block("14b", max(3, args.steps // 10), 1, dev, form="qkpv8")
     xch = bench_exchange(max(5, args.steps // 5), 2, dev)
     stk = bench_stack(max(3, args.steps // 10), 1, dev)
     stk14 = bench_stack(3, 1, dev, "14b")
@@ -847,6 +850,7 @@ def main() -> None:
                              "re-noising between DMD steps included; ramp-up and drain ticks hold fewer passes",
             "dit_block_1p3b_ms_per_chunk": round(b13["ms"], 4),
             "dit_block_14b_ms_per_chunk": round(b14["ms"], 4),
+            "dit_block_14b_qkpv8_ms_per_chunk": round(b14p["ms"], 4),
             "dit_block_note": "one block, 4680-token 3-frame chunk, 37440-key FP8 paged self-attn context, "
                               "512-token text cross-attn, all linears W8A8 int8, random init; includes a 9.4/31 MB "
                               "copy to reset x each step",
