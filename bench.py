@@ -199,6 +199,120 @@ def bench_gemm_data(steps: int, warmup: int, dev: str):
     return res
 
 
+def _library_call(fn, steps: int, warmup: int, reps: int, own: bool = False):
+    """ms per call of a vendor-library routine, or the error text when this torch build cannot run it here
+    (``own``: this library's kernel, whose errors propagate)."""
+    if own:
+        return _timed(lambda: [fn() for _ in range(reps)], steps, warmup) / reps, None
+    try:
+        fn()
+        torch.cuda.synchronize()
+    except (RuntimeError, NotImplementedError) as e:
+        return None, f"{type(e).__name__}: {str(e).splitlines()[0][:160]}"
+    return _timed(lambda: [fn() for _ in range(reps)], steps, warmup) / reps, None
+
+
+def bench_library(steps: int, warmup: int, dev: str):
+    """Vendor-library counterparts of the hot kernels on the same GPU, shapes and data, each beside this
+    library's kernel timed in the same way:
+
+    * torch._int_mm (hipBLASLt int8 x int8 -> int32, no scales) against the W8A8 GEMM with its fused
+      dequant + bias epilogue at the 1.3B linear 4680 x 1536 x 1536;
+    * the reference's per-tensor e4m3 linear as it calls it, torch._scaled_mm(x_fp8, w_fp8.t(), s_x, s_w,
+      bias, bf16) (wave_rt/runtime/fp8.py:49-56), against wf_gemm_fp8_pertensor on the same codes;
+    * torch's fused bf16 attention (scaled_dot_product_attention restricted to its flash and
+      memory-efficient backends; the unfused math path is never used) over the dequantized pages, the
+      reference's non-Sage attention after its gather-dequant, against the paged FP8 kernel's three forms
+      on the same pages (Q [4680, 12, 128] over 37440 keys)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from waveforcing_amd.backend import attn_paged_fp8
+    from waveforcing_amd.fp8 import (WaveFp8Linear, WaveW8A8Linear, _quant_rows_i8, gemm_fp8_pertensor,
+                                     gemm_i8)
+    from waveforcing_amd.kv import PagedKV
+
+    res = {}
+    x, w, b = inputs.linear_1p3b()
+    x, w, b = x.to(dev), w.to(dev), b.to(dev)
+    M, K = x.shape
+    N = w.shape[0]
+    ops = 2.0 * M * N * K
+    lin = WaveW8A8Linear(w, b)
+    qx, sx = _quant_rows_i8(x)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    wt = lin.w_i8.t()
+    reps = 50
+    for name, fn in (("w8a8_gemm", lambda: gemm_i8(qx, lin.w_i8, sx, lin.w_scale, lin.bias, out=y)),
+                     ("torch_int_mm", lambda: torch._int_mm(qx, wt))):
+        ms, err = _library_call(fn, steps, warmup, reps, own=name == "w8a8_gemm")
+        res[f"{name}_us"] = None if ms is None else round(ms * 1e3, 2)
+        res[f"{name}_tops"] = None if ms is None else round(ops / (ms * 1e-3) / 1e12, 1)
+        if err:
+            res[f"{name}_error"] = err
+    f8 = WaveFp8Linear(w, b)
+    from waveforcing_amd import _lib
+    from waveforcing_amd.fp8 import fp8_quant_pertensor
+
+    xc, xs = fp8_quant_pertensor(x, _lib.FP8_TENSOR_ACT)
+    w8t = f8.w_fp8.t()
+    for name, fn in (("fp8_gemm", lambda: gemm_fp8_pertensor(xc, f8.w_fp8, xs, f8.w_scale, f8.bias, out=y)),
+                     ("torch_scaled_mm", lambda: torch._scaled_mm(xc, w8t, scale_a=xs, scale_b=f8.w_scale,
+                                                                   bias=f8.bias, out_dtype=torch.bfloat16))):
+        ms, err = _library_call(fn, steps, warmup, reps, own=name == "fp8_gemm")
+        res[f"{name}_us"] = None if ms is None else round(ms * 1e3, 2)
+        res[f"{name}_tflops"] = None if ms is None else round(ops / (ms * 1e-3) / 1e12, 1)
+        if err:
+            res[f"{name}_error"] = err
+    if res.get("torch_scaled_mm_us") is not None:
+        ref = torch._scaled_mm(xc, w8t, scale_a=xs, scale_b=f8.w_scale, bias=f8.bias, out_dtype=torch.bfloat16)
+        mine = gemm_fp8_pertensor(xc, f8.w_fp8, xs, f8.w_scale, f8.bias)
+        res["fp8_gemm_vs_torch_scaled_mm_max_rel"] = float(
+            ((mine.float() - ref.float()).abs().max() / ref.float().abs().max()).item())
+    del x, w, y, qx, xc, lin, f8
+
+    H = HEADS
+    n_kv = TOKENS * 8
+    pages = n_kv // PAGE
+    pool = Fp8PagePool(2 * pages, H, HEAD_DIM, PAGE, dev)
+    table = pool.page_table(inputs.page_table(pages, 2 * pages, seed=11))
+    g = torch.Generator().manual_seed(12)
+    k = torch.randn((n_kv, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn((n_kv, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    pool.pack(k, v, table)
+    del k, v
+    q = torch.randn((TOKENS, H, HEAD_DIM), generator=g).to(torch.bfloat16).to(dev)
+    ctx = PagedKV(pool, table, n_kv)
+    out = torch.empty_like(q)
+    flops = 4.0 * TOKENS * n_kv * H * HEAD_DIM
+    for form, kw in ATTN_FORMS.items():
+        ms, _ = _library_call(lambda: attn_paged_fp8(q, ctx, out=out, **kw), steps, warmup, 1, own=True)
+        res[f"attn_paged_fp8_{form}_ms"] = round(ms, 4)
+    kd, vd = pool.unpack(table, n_kv)
+    qh = q.transpose(0, 1).unsqueeze(0).contiguous()
+    kh = kd.transpose(0, 1).unsqueeze(0).contiguous()
+    vh = vd.transpose(0, 1).unsqueeze(0).contiguous()
+    del kd, vd
+    for name, backend in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        def sdpa(backend=backend):
+            with sdpa_kernel([backend]):
+                return torch.nn.functional.scaled_dot_product_attention(qh, kh, vh)
+        ms, err = _library_call(sdpa, steps, warmup, 1)
+        res[f"torch_sdpa_{name}_ms"] = None if ms is None else round(ms, 4)
+        if ms is not None:
+            res[f"torch_sdpa_{name}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+            o_ref = sdpa()[0].transpose(0, 1).float()
+            attn_paged_fp8(q, ctx, out=out)
+            torch.cuda.synchronize()
+            res[f"attn_bf16_vs_torch_sdpa_{name}_max_abs"] = float((out.float() - o_ref).abs().max().item())
+        if err:
+            res[f"torch_sdpa_{name}_error"] = err
+    res["note"] = ("vendor-library routines on the same GPU and data: torch._int_mm (hipBLASLt, int32 out, no "
+                   "epilogue) and the reference's torch._scaled_mm e4m3 linear at 4680x1536x1536; torch's fused "
+                   "bf16 SDPA (flash / memory-efficient backends only) over the unpacked pages at 4680 queries x "
+                   "37440 keys x 12 heads, beside this library's kernels")
+    return res
+
+
 def bench_block_linears(steps: int, warmup: int, dev: str):
     """The Wan-1.3B block's W8A8 GEMMs on one 4680-token chunk as the block runs them: fused QKV [4608, 1536],
     O [1536, 1536], fc_in [8960, 1536], fc_out [1536, 8960] (activations pre-quantized; 345.97 G int8 ops per
@@ -679,7 +793,7 @@ def main() -> None:
                                        "tick_1p3b", "generate_1p3b", "copy", "attention_qk8", "block_1p3b_qk8",
                                        "attention_qkpv8", "block_1p3b_qkpv8", "block_14b_qkpv8", "dit_1p3b_qkpv8",
                                        "kv_pertensor",
-                                       "attention_data", "gemm_data"],
+                                       "attention_data", "gemm_data", "library"],
                     help="run one workload alone (for profiler runs) and print its own JSON line")
     args = ap.parse_args()
     WARM_SECONDS = args.warm_seconds
@@ -705,6 +819,7 @@ def main() -> None:
               "attention_qkpv8": lambda s, w, d: bench_attention(s, w, d, form="qkpv8"),
               "block_1p3b_qkpv8": lambda s, w, d: bench_block("1.3b", s, w, d, form="qkpv8"),
               "block_14b_qkpv8": lambda s, w, d: bench_block("14b", s, w, d, form="qkpv8"),
+              "library": bench_library,
               "dit_1p3b_qkpv8": lambda s, w, d: bench_dit(s, w, d, form="qkpv8"),
               "kv_pertensor": bench_kv_pertensor, "attention_data": bench_attention_data,
               "gemm_data": bench_gemm_data,
@@ -732,6 +847,7 @@ def main() -> None:
     gen = bench_generate(1, 1, dev)
     gdat = bench_gemm_data(max(3, args.steps // 20), 2, dev)
     adat = bench_attention_data(max(5, args.steps // 5), 2, dev, repeats=1)
+    libr = bench_library(max(5, args.steps // 5), 2, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_kv()
     cpu_extra = None if args.no_cpu_baseline else cpu_baseline_extra()
     # one launch per step: the launch duration is the step time
@@ -861,6 +977,7 @@ def main() -> None:
             "attn_power": {**{k.replace("_ms_0", "_ms"): v for k, v in adat.items()},
                            "note": "the three attention forms on the attention workload with N(0,1) or zero K / V "
                                    "in the pages, each after a second of sustained launches"},
+            "library": libr,
         },
     }
     print(json.dumps(line), flush=True)
