@@ -263,6 +263,31 @@ def bench_library(steps: int, warmup: int, dev: str):
         res[f"{name}_tflops"] = None if ms is None else round(ops / (ms * 1e-3) / 1e12, 1)
         if err:
             res[f"{name}_error"] = err
+    # the 14B fc_out, 4680 x 5120 x 13824 (long K), on N(0, 1) activations and weights drawn on the GPU
+    gen = torch.Generator(device=dev).manual_seed(5)
+    M2, N2, K2 = TOKENS, 5120, 13824
+    ops2 = 2.0 * M2 * N2 * K2
+    x2 = torch.randn((M2, K2), generator=gen, device=dev).to(torch.bfloat16)
+    w2 = (torch.randn((N2, K2), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    y2 = torch.empty((M2, N2), dtype=torch.bfloat16, device=dev)
+    qx2, sx2 = _quant_rows_i8(x2)
+    qw2, sw2 = _quant_rows_i8(w2)
+    xc2, xs2 = fp8_quant_pertensor(x2, _lib.FP8_TENSOR_ACT)
+    wc2, ws2 = fp8_quant_pertensor(w2, _lib.FP8_TENSOR_WEIGHT)
+    del x2, w2
+    qw2t, wc2t = qw2.t(), wc2.t()
+    for name, fn, unit in (
+            ("14b_fc_out_w8a8_gemm", lambda: gemm_i8(qx2, qw2, sx2, sw2, None, out=y2), "tops"),
+            ("14b_fc_out_torch_int_mm", lambda: torch._int_mm(qx2, qw2t), "tops"),
+            ("14b_fc_out_fp8_gemm", lambda: gemm_fp8_pertensor(xc2, wc2, xs2, ws2, None, out=y2), "tflops"),
+            ("14b_fc_out_torch_scaled_mm", lambda: torch._scaled_mm(xc2, wc2t, scale_a=xs2, scale_b=ws2,
+                                                                     out_dtype=torch.bfloat16), "tflops")):
+        ms, err = _library_call(fn, steps, warmup, 3, own="torch" not in name)
+        res[f"{name}_us"] = None if ms is None else round(ms * 1e3, 2)
+        res[f"{name}_{unit}"] = None if ms is None else round(ops2 / (ms * 1e-3) / 1e12, 1)
+        if err:
+            res[f"{name}_error"] = err
+    del qx2, qw2, xc2, wc2, y2
     if res.get("torch_scaled_mm_us") is not None:
         ref = torch._scaled_mm(xc, w8t, scale_a=xs, scale_b=f8.w_scale, bias=f8.bias, out_dtype=torch.bfloat16)
         mine = gemm_fp8_pertensor(xc, f8.w_fp8, xs, f8.w_scale, f8.bias)
@@ -307,7 +332,8 @@ def bench_library(steps: int, warmup: int, dev: str):
         if err:
             res[f"torch_sdpa_{name}_error"] = err
     res["note"] = ("vendor-library routines on the same GPU and data: torch._int_mm (hipBLASLt, int32 out, no "
-                   "epilogue) and the reference's torch._scaled_mm e4m3 linear at 4680x1536x1536; torch's fused "
+                   "epilogue) and the reference's torch._scaled_mm e4m3 linear at 4680x1536x1536 and at the 14B "
+                   "fc_out 4680x5120x13824 (no bias there); torch's fused "
                    "bf16 SDPA (flash / memory-efficient backends only) over the unpacked pages at 4680 queries x "
                    "37440 keys x 12 heads, beside this library's kernels")
     return res

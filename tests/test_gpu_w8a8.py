@@ -67,6 +67,10 @@ def _gemm_case(M, N, K, seed, bias=True, gelu=False):
     (1, 4, 16), (17, 132, 48), (300, 256, 1552), (513, 1540, 272),
     (3000, 3204, 272),    # more tiles than CUs (several rounds), partial tiles, N % 8 == 4: 8-byte stores
     (2050, 8196, 160),    # 561 tiles, K tail of 32 bytes
+    # shapes that take the 256 x 256 workgroup tile (two LDS stages): the 1.3B fc_in, its M / N / K tails
+    # (72 rows in the last tile row, a 252-column last tile with N % 8 == 4, a 16-byte K tail), and K loops
+    # of one and two steps
+    (4680, 8960, 1536), (4680, 8956, 1552), (4680, 8960, 16), (4680, 8960, 144),
 ])
 def test_gemm_exact(M, N, K):
     y, acc, oy, oacc = _gemm_case(M, N, K, seed=M + N + K)

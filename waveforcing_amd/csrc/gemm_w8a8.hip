@@ -15,9 +15,11 @@
 // torch._scaled_mm(x_fp8, w_fp8.t(), scale_a, scale_b, bias, bf16) at
 // wave_rt/runtime/fp8.py:49-56.
 //
-// Structure (one 128 x 256 output tile per workgroup of 8 waves, each wave
-// 64 x 64 as 2 x 2 blocks of 32 x 32 MFMAs: v_mfma_i32_32x32x32_i8, or
-// v_mfma_f32_32x32x64_f8f6f4 with e4m3 operands; both operands K-contiguous):
+// Structure (one 128 x 256 or 256 x 256 output tile per workgroup of 8 waves,
+// each wave 64 x 64 or 128 x 64 as 2 x 2 or 4 x 2 blocks of 32 x 32 MFMAs:
+// v_mfma_i32_32x32x32_i8, or v_mfma_f32_32x32x64_f8f6f4 with e4m3 operands;
+// both operands K-contiguous; the host picks the tile per shape, see
+// use_big_tile):
 //  * Global -> LDS by DMA (buffer_load_dwordx4 ... lds): each instruction
 //    moves 1 KB = 8 rows x 128 K-bytes into a contiguous LDS block, no
 //    registers involved.  Lane l lands at byte 16 l, i.e. row l/8, position
@@ -28,7 +30,7 @@
 //  * Prologue: the waves that win the issue arbitration of their SIMD (0..3)
 //    fetch all of stage 0, their SIMD mates stage 1, so the first stage is
 //    not queued behind the second.
-//  * Three LDS stages of 48 KB.  A K step (128 bytes) is SUB sub-steps of one
+//  * Three LDS stages of 48 KB (the 256-row tile: two of 64 KB, see Tile).  A K step (128 bytes) is SUB sub-steps of one
 //    MFMA depth (4 x 32 bytes for int8, 2 x 64 for e4m3); fragments of
 //    sub-step g+1 are read while the MFMAs of g issue, the reads and DMAs
 //    spread between the MFMAs.  A lane's operand bytes are the same K
@@ -43,9 +45,9 @@
 //    scales and bias reach LDS by DMA (three instructions, not a copy per
 //    lane, which would queue ~100 KB per CU ahead of the first stage);
 //    results are converted with v_cvt_pk_bf16_f32 (round to nearest even);
-//    each wave stages 32-row slabs of its 64 x 64 sub-tile in its own LDS
-//    area and stores them as full 128-byte row segments while it converts
-//    the next slab.
+//    each wave stages 32-row slabs of its sub-tile in its own LDS area (two
+//    slab areas in turn) and stores them as full 128-byte row segments while
+//    it converts the next slab.
 //  * Tiles are ordered so that the workgroups one XCD receives (blockIdx % 8)
 //    form a contiguous range, walked in bands of 8 tile rows, so co-resident
 //    workgroups share A and W panels in that XCD's L2.  Shapes with more
@@ -75,26 +77,39 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int BK = 128;  // K bytes per step
-constexpr int BM = 128, BN = 256, WM = 2, WN = 4;
-constexpr int NW = WM * WN;
-constexpr int THREADS = NW * 64;
-constexpr int MI = BM / WM / 32, NI = BN / WN / 32;  // 32x32 blocks per wave
-constexpr int A_BYTES = BM * BK;
-constexpr int STAGE = (BM + BN) * BK;
-constexpr int ST = 3;
-constexpr int NBA = BM / 8 / NW, NBB = BN / 8 / NW;  // 1 KB DMA blocks per wave and step
-constexpr int NDMA = NBA + NBB;
 constexpr int GROUP_M = 8;
 constexpr int NUM_XCD = 8;
-constexpr int OUT_PITCH = BN * 2 + 16;  // bf16 epilogue tile row pitch (bytes)
-static_assert(NBA * 8 * NW == BM && NBB * 8 * NW == BN, "DMA blocks");
-static_assert(BM * OUT_PITCH <= ST * STAGE, "epilogue tile fits the stages");
-// The one-round kernel's per-column epilogue operands in LDS, past the stages: sw (fp32) at 0, the bias
-// as it arrives (bf16) at 1024 and converted to fp32 at 2048.
+// The per-column epilogue operands in LDS, past the stages: sw (fp32) at 0, the bias as it arrives (bf16)
+// at 1024 and converted to fp32 at 2048.
 constexpr int EPI_BYTES = 3072;
-// Per-wave output staging of the one-round kernel: two 32-row slabs of the wave's 64 x 64 sub-tile.
-constexpr int WPITCH = BN / WN * 2 + 16;
-static_assert(NW * 2 * 32 * WPITCH <= ST * STAGE, "wave staging fits the stages");
+
+// Workgroup tile: BM x 256 outputs, 8 waves in 2 x 4, each (BM / 2) x 64 as MI x 2 blocks of 32 x 32;
+// ST LDS stages of (BM + 256) x 128 bytes.
+//  * Tile<128, 3>: 48 KB stages; the DMA of step j is spread over the last sub-step of step j-3 and the
+//    first SUB-1 sub-steps of step j-2.
+//  * Tile<256, 2>: 64 KB stages, a third fewer operand bytes per MFMA through the vector-memory path (64 KB
+//    per 256 MFMAs instead of 48 KB per 128); the DMA of step j is issued in the last sub-step of step j-2,
+//    right after the barrier that frees its stage, and is waited for at step j-1's barrier.
+template <int BM_, int ST_>
+struct Tile {
+  static constexpr int BM = BM_, BN = 256, WM = 2, WN = 4;
+  static constexpr int NW = WM * WN;
+  static constexpr int THREADS = NW * 64;
+  static constexpr int MI = BM / WM / 32, NI = BN / WN / 32;  // 32x32 blocks per wave
+  static constexpr int A_BYTES = BM * BK;
+  static constexpr int STAGE = (BM + BN) * BK;
+  static constexpr int ST = ST_;
+  static constexpr int NBA = BM / 8 / NW, NBB = BN / 8 / NW;  // 1 KB DMA blocks per wave and step
+  static constexpr int NDMA = NBA + NBB;
+  // Per-wave output staging: two 32-row slabs of the wave's sub-tile, used in turn.
+  static constexpr int WPITCH = BN / WN * 2 + 16;
+  static_assert(ST == 2 || ST == 3, "two or three stages");
+  static_assert(NBA * 8 * NW == BM && NBB * 8 * NW == BN, "DMA blocks");
+  static_assert(NW * 2 * 32 * WPITCH <= ST * STAGE, "wave staging fits the stages");
+  static_assert(ST * STAGE + EPI_BYTES <= 160 * 1024, "LDS of one workgroup");
+};
+using TileStd = Tile<128, 3>;
+using TileBig = Tile<256, 2>;
 // Word 3 of a raw (untyped, stride 0) buffer resource on gfx9-family parts:
 // DATA_FORMAT = 32 bit.  With it, offsets >= num_records read as zero.
 constexpr int kBufferRsrcWord3 = 0x00020000;
@@ -166,7 +181,7 @@ struct GemmArgs {
 // Stamp `slot` of this workgroup's phase record (instrumented build only; a no-op otherwise).
 __device__ inline void phase_stamp(const GemmArgs& p, int wave, int lane, int slot) {
 #ifdef WF_GEMM_PHASES
-  if (p.phases != nullptr && (wave == 0 || wave == NW / 2)) {
+  if (p.phases != nullptr && (wave == 0 || wave == 4)) {
     // wave 0: the shader clock (cycles); its SIMD mate: the constant 100 MHz reference clock at the same
     // points (the same barriers), which turns the cycle counts into a frequency
     const uint64_t t = wave == 0 ? __builtin_amdgcn_s_memtime() : __builtin_amdgcn_s_memrealtime();
@@ -199,8 +214,11 @@ __device__ inline void epi_dma(const GemmArgs& p, int wave, int lane, int n0, ui
   }
 }
 
-template <typename OP, bool HAS_BIAS, bool GELU, bool ACC>
-__global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
+template <typename T, typename OP, bool HAS_BIAS, bool GELU, bool ACC>
+__global__ __launch_bounds__(T::THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
+  constexpr int BM = T::BM, BN = T::BN, WM = T::WM, WN = T::WN, NW = T::NW, MI = T::MI, NI = T::NI;
+  constexpr int A_BYTES = T::A_BYTES, STAGE = T::STAGE, ST = T::ST, NBA = T::NBA, NDMA = T::NDMA;
+  constexpr int WPITCH = T::WPITCH;
   constexpr bool kI8 = std::is_same<OP, OpI8>::value;
   constexpr int SUB = OP::SUB;
   constexpr int PIECES = OP::PIECES;
@@ -308,14 +326,15 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   };
   // The MFMAs of buffer B with, spread between them, the reads of sub-step rs
   // of rstage into buffer 1-B and DMA slot SLOT (of SUB per step) for the
-  // step at K offset dk0 into dstage.
+  // step at K offset dk0 into dstage.  Three stages spread a step's DMAs evenly over the SUB slots; two
+  // stages put them all in slot 0 (the sub-step right after the barrier), for the longest lead.
   // RD / DM switch the reads and the DMAs off (the last steps have no next sub-step or step to fetch).
   auto substep = [&](auto B, int rstage, int rs, auto SLOT, int dk0, int dstage, auto RD, auto DM) {
     constexpr int b = decltype(B)::value;
     constexpr int slot = decltype(SLOT)::value;
     constexpr bool rd = decltype(RD)::value, dm = decltype(DM)::value;
-    constexpr int d_lo = (slot * NDMA + SUB - 1) / SUB;
-    constexpr int d_hi = dm ? ((slot + 1) * NDMA + SUB - 1) / SUB : d_lo;
+    constexpr int d_lo = ST == 3 ? (slot * NDMA + SUB - 1) / SUB : 0;
+    constexpr int d_hi = !dm ? d_lo : ST == 3 ? ((slot + 1) * NDMA + SUB - 1) / SUB : (slot == 0 ? NDMA : 0);
     constexpr int NMF = MI * NI, NRD = rd ? (MI + NI) * PIECES : 0;
     constexpr int NOPS = NRD + d_hi - d_lo;
     static_for<NMF>([&](auto Q) {
@@ -365,10 +384,13 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
                       __uint_as_float(b.y & 0xffff0000u));
     }
   }
-  if (nk >= 3) static_for<(NDMA + SUB - 1) / SUB>([&](auto J) { dma(J, 2 * BK, 2); });
+  if constexpr (ST == 3) {
+    if (nk >= 3) static_for<(NDMA + SUB - 1) / SUB>([&](auto J) { dma(J, 2 * BK, 2); });
+  }
   static_for<(MI + NI) * PIECES>([&](auto O) { frag_read(O, ic<0>{}, 0, 0); });
   __builtin_amdgcn_sched_barrier(0);
 
+  if constexpr (ST == 3) {
   // Step kb: sub-steps 1..SUB-1 fetch slots 1.. of step kb+2 (PRE), the last sub-step, after the barrier,
   // slot 0 of step kb+3 (POST).  Only steps below nk are fetched, so the last three steps are peeled:
   // step nk-3 has no POST, step nk-2 neither, and step nk-1 also no barrier and no fragment reads.
@@ -402,6 +424,34 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   if (nk >= 3) step(kb++, ic<1>{}, ic<0>{}, ic<0>{});
   if (nk >= 2) step(kb++, ic<0>{}, ic<0>{}, ic<0>{});
   step(kb, ic<0>{}, ic<0>{}, ic<1>{});
+  } else {
+  // Two stages.  Step kb: sub-steps 1..SUB-1 read from stage c0 and fetch nothing; at the barrier every DMA
+  // issued so far (step kb+1's) has landed and every wave is done with c0; the last sub-step reads
+  // sub-step 0 of step kb+1 from c1 and fetches all of step kb+2 into c0 (POST).  Peeled: step nk-2 has
+  // no POST, step nk-1 no barrier and no fragment reads.
+  int c0 = 0, c1 = 1;  // stages of steps kb, kb+1
+  auto step = [&](int kb, auto POST, auto LAST) {
+    constexpr bool last = decltype(LAST)::value;
+    static_for<SUB - 1>([&](auto S) {
+      constexpr int s = decltype(S)::value;
+      substep(ic<s & 1>{}, c0, s + 1, ic<s + 1>{}, 0, 0, ic<1>{}, ic<0>{});
+    });
+    if constexpr (!last) {
+      wait_counts<0, 0>();
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    substep(ic<(SUB - 1) & 1>{}, c1, 0, ic<0>{}, (kb + 2) * BK, c0, ic<!last>{}, POST);
+    const int c = c0;
+    c0 = c1;
+    c1 = c;
+  };
+  int kb = 0;
+  for (; kb < nk - 2; ++kb) step(kb, ic<1>{}, ic<0>{});
+  if (nk >= 2) step(kb++, ic<0>{}, ic<0>{});
+  step(kb, ic<0>{}, ic<1>{});
+  }
   // The epilogue operands from LDS, then all DMAs landed, all LDS accesses done and all waves past
   // their last LDS read before the stages are reused for the output staging.  The fp32 bias is wave 1's
   // write after the prologue barrier: with two or more K steps the first step's barrier (after an LDS
@@ -431,7 +481,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   uint8_t* const wst = lds + wave * (2 * 32 * WPITCH);
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
-    uint8_t* const slab = wst + i * 32 * WPITCH;
+    // slabs alternate between two areas: a wave's LDS accesses execute in order, so slab i + 2's writes
+    // follow slab i's read-back
+    uint8_t* const slab = wst + (i & 1) * 32 * WPITCH;
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
@@ -509,27 +561,68 @@ GemmArgs make_args(const void* a, const void* w, int64_t M, int64_t N, int64_t K
   return p;
 }
 
-template <typename OP, bool ACC>
-void launch_kernel(const GemmArgs& p, bool bias, bool gelu, dim3 grid, hipStream_t stream) {
-  const dim3 block(THREADS);
+template <typename T, typename OP, bool ACC>
+void launch_kernel(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream) {
+  const int64_t tiles = ((static_cast<int64_t>(p.M) + T::BM - 1) / T::BM) * ((p.N + T::BN - 1) / T::BN);
+  const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD));
+  const dim3 block(T::THREADS);
   if (bias && gelu)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, true, true, ACC>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((gemm_w8a8_kernel<T, OP, true, true, ACC>), grid, block, 0, stream, p);
   else if (bias)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, true, false, ACC>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((gemm_w8a8_kernel<T, OP, true, false, ACC>), grid, block, 0, stream, p);
   else if (gelu)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, false, true, ACC>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((gemm_w8a8_kernel<T, OP, false, true, ACC>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, false, false, ACC>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((gemm_w8a8_kernel<T, OP, false, false, ACC>), grid, block, 0, stream, p);
+}
+
+// Tile choice: -1 by the rounds model below; 0 / 1 force the 128- / 256-row tile (settable only in the
+// instrumented library, for A/B runs).
+int g_tile_policy = -1;
+
+// Compute units of the current device (one workgroup per CU at a time), cached per device.
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n
+                                                                                                             : 256;
+  }
+  return cus[dev];
+}
+
+// Both tiles run one workgroup per CU, so a launch takes about ceil(tiles / CUs) rounds of its tile's time.
+// A 256-row tile holds twice the work of a 128-row tile and takes about kBigTileCost times as long (1.67-1.81
+// on the eight Wan-1.3B / 14B linears at 4680 tokens, int8 and e4m3 alike); it is chosen when its rounds
+// cost at least kBigTileMargin less.  On those shapes that picks it for the 1.3B fc_in only (6 rounds of
+// 128-row tiles against 3 of 256-row tiles: 10-11 % faster); the others measured equal or slower with it.
+constexpr double kBigTileCost = 1.75;
+constexpr double kBigTileMargin = 0.95;
+bool use_big_tile(const GemmArgs& p) {
+  if (g_tile_policy >= 0) return g_tile_policy == 1;
+  const int64_t cus = device_cus();
+  const int64_t tn = (p.N + 255) / 256;
+  const int64_t rounds_std = ((static_cast<int64_t>(p.M) + 127) / 128 * tn + cus - 1) / cus;
+  const int64_t rounds_big = ((static_cast<int64_t>(p.M) + 255) / 256 * tn + cus - 1) / cus;
+  return static_cast<double>(rounds_big) * kBigTileCost < kBigTileMargin * static_cast<double>(rounds_std);
 }
 
 template <typename OP>
 int launch(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream, const char* fn) {
-  const int64_t tiles = ((static_cast<int64_t>(p.M) + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD));
-  if (std::is_same<OP, OpI8>::value && p.acc_out != nullptr)
-    launch_kernel<OP, true>(p, bias, gelu, grid, stream);
-  else
-    launch_kernel<OP, false>(p, bias, gelu, grid, stream);
+  const bool acc = std::is_same<OP, OpI8>::value && p.acc_out != nullptr;
+  if (use_big_tile(p)) {
+    if (acc)
+      launch_kernel<TileBig, OP, true>(p, bias, gelu, stream);
+    else
+      launch_kernel<TileBig, OP, false>(p, bias, gelu, stream);
+  } else {
+    if (acc)
+      launch_kernel<TileStd, OP, true>(p, bias, gelu, stream);
+    else
+      launch_kernel<TileStd, OP, false>(p, bias, gelu, stream);
+  }
   return check_launch(fn);
 }
 
@@ -651,6 +744,15 @@ extern "C" int wf_fp8_linear_pertensor(const void* x, int64_t m, int64_t k, int6
 // for the phase stamps of the following GEMM launches, or null to stop recording.
 extern "C" int wf_gemm_set_phase_buffer(uint64_t* stamps) {
   wf::g_phase_buffer = stamps;
+  return WF_OK;
+}
+#endif
+#if defined(WF_GEMM_PHASES) || defined(WF_GEMM_TILE_LAB)
+// Instrumented builds only: the workgroup tile of the following GEMM launches (-1 the product's choice,
+// 0 the 128 x 256 tile, 1 the 256 x 256 tile).
+extern "C" int wf_gemm_set_tile_policy(int policy) {
+  WF_REQUIRE(policy >= -1 && policy <= 1, WF_E_INVALID, "wf_gemm_set_tile_policy: policy %d not in -1..1", policy);
+  wf::g_tile_policy = policy;
   return WF_OK;
 }
 #endif

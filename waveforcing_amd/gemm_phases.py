@@ -46,6 +46,11 @@ def _lib(path: str | None = None):
     lib.wf_gemm_i8.argtypes = [vp, vp, i64, i64, i64, vp, vp, vp, vp, i64, vp, i32, vp]
     lib.wf_gemm_fp8_pertensor.argtypes = [vp, vp, i64, i64, i64, vp, vp, vp, vp, i64, vp]
     lib.wf_gemm_set_phase_buffer.argtypes = [vp]
+    lib.wf_gemm_set_tile_policy.argtypes = [i32]
+    # the stamps below are read as 128 x 256 tiles of 8 waves: force that tile (the product picks the
+    # 256 x 256 tile for some shapes; waveforcing_amd.gemm_tiles compares the two)
+    if lib.wf_gemm_set_tile_policy(0) != 0:
+        raise RuntimeError("wf_gemm_set_tile_policy failed")
     return lib
 
 
