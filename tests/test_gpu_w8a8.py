@@ -71,6 +71,10 @@ def _gemm_case(M, N, K, seed, bias=True, gelu=False):
     # (72 rows in the last tile row, a 252-column last tile with N % 8 == 4, a 16-byte K tail), and K loops
     # of one and two steps
     (4680, 8960, 1536), (4680, 8956, 1552), (4680, 8960, 16), (4680, 8960, 144),
+    # shapes planned as whole rounds of 256 x 256 tiles plus a second launch of 128 x 256 tiles over the rest
+    # (on 256 CUs): one round and a partly covered tile row (N = 5120, the 14B O / fc_out), four rounds
+    # (N = 15360, the 14B QKV), three rounds (N = 13824, the 14B fc_in); every output element compared
+    (4680, 5120, 512), (4680, 15360, 256), (4680, 13824, 272),
 ])
 def test_gemm_exact(M, N, K):
     y, acc, oy, oacc = _gemm_case(M, N, K, seed=M + N + K)

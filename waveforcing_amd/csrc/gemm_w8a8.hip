@@ -18,8 +18,9 @@
 // Structure (one 128 x 256 or 256 x 256 output tile per workgroup of 8 waves,
 // each wave 64 x 64 or 128 x 64 as 2 x 2 or 4 x 2 blocks of 32 x 32 MFMAs:
 // v_mfma_i32_32x32x32_i8, or v_mfma_f32_32x32x64_f8f6f4 with e4m3 operands;
-// both operands K-contiguous; the host picks the tile per shape, see
-// use_big_tile):
+// both operands K-contiguous; the host plans the tiles per shape, see
+// plan_tiles: one tile for the whole output, or whole rounds of 256-row
+// tiles followed by a launch of 128-row tiles over the rest):
 //  * Global -> LDS by DMA (buffer_load_dwordx4 ... lds): each instruction
 //    moves 1 KB = 8 rows x 128 K-bytes into a contiguous LDS block, no
 //    registers involved.  Lane l lands at byte 16 l, i.e. row l/8, position
@@ -164,6 +165,12 @@ __device__ inline void dma4(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds_block, int
 }
 
 
+// A rectangle of the output that one launch covers with its workgroup tile: rows [m0, m1), columns [n0, n1);
+// m0 and n0 lie on the launch's tile grid and every tile but those at M or N lies wholly inside.
+struct Rect {
+  int m0, m1, n0, n1;
+};
+
 struct GemmArgs {
   const void* a;         // [M, K] int8 or e4m3
   const void* w;         // [N, K]
@@ -176,6 +183,8 @@ struct GemmArgs {
   int64_t ldy;
   int vec16;             // y and ldy allow 16-byte row stores
   uint64_t* phases;      // phase-timing stamps (instrumented build only), or null
+  Rect rect[2];          // the output this launch covers: rect[0], then rect[1] when n_rect == 2
+  int n_rect;
 };
 
 // Stamp `slot` of this workgroup's phase record (instrumented build only; a no-op otherwise).
@@ -227,18 +236,24 @@ __global__ __launch_bounds__(T::THREADS, 1) void gemm_w8a8_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[ST * STAGE + EPI_BYTES];
   uint8_t* const epi = lds + ST * STAGE;
 
-  const int tiles_m = (p.M + BM - 1) / BM;
-  const int tiles_n = (p.N + BN - 1) / BN;
-  const int n_tiles = tiles_m * tiles_n;
+  // The launch's tiles: those of rect[0], then those of rect[1].
+  const int tm0 = (p.rect[0].m1 - p.rect[0].m0 + BM - 1) / BM, tn0 = (p.rect[0].n1 - p.rect[0].n0 + BN - 1) / BN;
+  const int tm1 = p.n_rect > 1 ? (p.rect[1].m1 - p.rect[1].m0 + BM - 1) / BM : 0;
+  const int tn1 = p.n_rect > 1 ? (p.rect[1].n1 - p.rect[1].n0 + BN - 1) / BN : 0;
+  const int c0 = tm0 * tn0;
+  const int n_tiles = c0 + tm1 * tn1;
   const int per_xcd = (n_tiles + NUM_XCD - 1) / NUM_XCD;
-  const int t = (blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
-  if (t >= n_tiles) return;
-  // Grouped order: bands of GROUP_M tile rows swept column by column.
+  const int t_all = (blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
+  if (t_all >= n_tiles) return;
+  const bool second = t_all >= c0;
+  const int t = second ? t_all - c0 : t_all;
+  const int tiles_m = second ? tm1 : tm0, tiles_n = second ? tn1 : tn0;
+  // Grouped order within the rectangle: bands of GROUP_M tile rows swept column by column.
   const int per_group = GROUP_M * tiles_n;
   const int first_m = (t / per_group) * GROUP_M;
   const int band = min(tiles_m - first_m, GROUP_M);
-  const int m0 = (first_m + (t % per_group) % band) * BM;
-  const int n0 = ((t % per_group) / band) * BN;
+  const int m0 = (second ? p.rect[1].m0 : p.rect[0].m0) + (first_m + (t % per_group) % band) * BM;
+  const int n0 = (second ? p.rect[1].n0 : p.rect[0].n0) + ((t % per_group) / band) * BN;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -558,12 +573,19 @@ GemmArgs make_args(const void* a, const void* w, int64_t M, int64_t N, int64_t K
   p.ldy = ldy;
   p.vec16 = (ldy % 8 == 0) && ((reinterpret_cast<uintptr_t>(y) & 15u) == 0);
   p.phases = g_phase_buffer;
+  p.rect[0] = Rect{0, p.M, 0, p.N};
+  p.rect[1] = Rect{0, 0, 0, 0};
+  p.n_rect = 1;
   return p;
 }
 
 template <typename T, typename OP, bool ACC>
 void launch_kernel(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream) {
-  const int64_t tiles = ((static_cast<int64_t>(p.M) + T::BM - 1) / T::BM) * ((p.N + T::BN - 1) / T::BN);
+  int64_t tiles = 0;
+  for (int r = 0; r < p.n_rect; ++r)
+    tiles += static_cast<int64_t>((p.rect[r].m1 - p.rect[r].m0 + T::BM - 1) / T::BM) *
+             ((p.rect[r].n1 - p.rect[r].n0 + T::BN - 1) / T::BN);
+  if (tiles == 0) return;
   const dim3 grid(static_cast<uint32_t>((tiles + NUM_XCD - 1) / NUM_XCD * NUM_XCD));
   const dim3 block(T::THREADS);
   if (bias && gelu)
@@ -576,8 +598,8 @@ void launch_kernel(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream) 
     hipLaunchKernelGGL((gemm_w8a8_kernel<T, OP, false, false, ACC>), grid, block, 0, stream, p);
 }
 
-// Tile choice: -1 by the rounds model below; 0 / 1 force the 128- / 256-row tile (settable only in the
-// instrumented library, for A/B runs).
+// Tile plan: -1 the cost model below; 0 / 1 force the 128- / 256-row tile for the whole output (settable only
+// in the instrumented libraries, for A/B runs).
 int g_tile_policy = -1;
 
 // Compute units of the current device (one workgroup per CU at a time), cached per device.
@@ -594,30 +616,90 @@ int device_cus() {
 }
 
 // Both tiles run one workgroup per CU, so a launch takes about ceil(tiles / CUs) rounds of its tile's time.
-// A 256-row tile holds twice the work of a 128-row tile and takes about kBigTileCost times as long (1.67-1.81
-// on the eight Wan-1.3B / 14B linears at 4680 tokens, int8 and e4m3 alike); it is chosen when its rounds
-// cost at least kBigTileMargin less.  On those shapes that picks it for the 1.3B fc_in only (6 rounds of
-// 128-row tiles against 3 of 256-row tiles: 10-11 % faster); the others measured equal or slower with it.
+// A 256-row tile holds twice the work of a 128-row tile and takes about kBigTileCost times as long (1.62-1.83
+// on the eight Wan-1.3B / 14B linears at 4680 tokens, int8 and e4m3 alike).  Plans: the 128-row tile
+// everywhere; the 256-row tile everywhere; or F whole rounds of 256-row tiles (F x CUs of them in row-major
+// order over the 256-row grid: whole tile rows, then a prefix of the next) followed by a second launch of
+// 128-row tiles over the rest (the suffix of that tile row and every row below), so that neither launch
+// ends on a mostly idle round.  The cheapest plan by the model is taken when it costs at least
+// kPlanMargin less than the 128-row tile alone.
 constexpr double kBigTileCost = 1.75;
-constexpr double kBigTileMargin = 0.95;
-bool use_big_tile(const GemmArgs& p) {
-  if (g_tile_policy >= 0) return g_tile_policy == 1;
+constexpr double kPlanMargin = 0.95;
+
+struct Plan {
+  int big_rects = 0;  // 0: no 256-row launch
+  Rect big[2];
+  int std_rects = 0;  // 0: no 128-row launch
+  Rect std_[2];
+};
+
+int64_t rect_tiles(const Rect& r, int bm) {
+  return static_cast<int64_t>((r.m1 - r.m0 + bm - 1) / bm) * ((r.n1 - r.n0 + 255) / 256);
+}
+
+Plan plan_tiles(int M, int N) {
+  Plan all_std;
+  all_std.std_rects = 1;
+  all_std.std_[0] = Rect{0, M, 0, N};
+  Plan all_big;
+  all_big.big_rects = 1;
+  all_big.big[0] = Rect{0, M, 0, N};
+  if (g_tile_policy == 0) return all_std;
+  if (g_tile_policy == 1) return all_big;
   const int64_t cus = device_cus();
-  const int64_t tn = (p.N + 255) / 256;
-  const int64_t rounds_std = ((static_cast<int64_t>(p.M) + 127) / 128 * tn + cus - 1) / cus;
-  const int64_t rounds_big = ((static_cast<int64_t>(p.M) + 255) / 256 * tn + cus - 1) / cus;
-  return static_cast<double>(rounds_big) * kBigTileCost < kBigTileMargin * static_cast<double>(rounds_std);
+  const int64_t tn = (N + 255) / 256;
+  const int64_t big_tiles = static_cast<int64_t>((M + 255) / 256) * tn;
+  const double cost_std = static_cast<double>((rect_tiles(all_std.std_[0], 128) + cus - 1) / cus);
+  Plan best = all_std;
+  double best_cost = cost_std;
+  const double cost_big = kBigTileCost * static_cast<double>((big_tiles + cus - 1) / cus);
+  if (cost_big < kPlanMargin * best_cost) {
+    best = all_big;
+    best_cost = cost_big;
+  }
+  for (int64_t f = 1; f * cus < big_tiles; ++f) {
+    const int64_t nb = f * cus;
+    const int full = static_cast<int>(nb / tn), part = static_cast<int>(nb % tn);
+    Plan pl;
+    const int row_a = 256 * full;                     // end of the whole 256-row tile rows
+    const int row_b = min(row_a + 256, M);            // end of the partly covered tile row
+    if (full > 0) pl.big[pl.big_rects++] = Rect{0, row_a, 0, N};
+    if (part > 0) {
+      pl.big[pl.big_rects++] = Rect{row_a, row_b, 0, 256 * part};
+      pl.std_[pl.std_rects++] = Rect{row_a, row_b, 256 * part, N};
+      if (row_b < M) pl.std_[pl.std_rects++] = Rect{row_b, M, 0, N};
+    } else if (row_a < M) {
+      pl.std_[pl.std_rects++] = Rect{row_a, M, 0, N};
+    }
+    int64_t ns = 0;
+    for (int r = 0; r < pl.std_rects; ++r) ns += rect_tiles(pl.std_[r], 128);
+    const double cost = kBigTileCost * static_cast<double>(f) + static_cast<double>((ns + cus - 1) / cus);
+    if (cost < kPlanMargin * cost_std && cost < best_cost) {
+      best = pl;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 template <typename OP>
-int launch(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream, const char* fn) {
-  const bool acc = std::is_same<OP, OpI8>::value && p.acc_out != nullptr;
-  if (use_big_tile(p)) {
+int launch(const GemmArgs& p0, bool bias, bool gelu, hipStream_t stream, const char* fn) {
+  const bool acc = std::is_same<OP, OpI8>::value && p0.acc_out != nullptr;
+  const Plan plan = plan_tiles(p0.M, p0.N);
+  GemmArgs p = p0;
+  if (plan.big_rects > 0) {
+    p.n_rect = plan.big_rects;
+    p.rect[0] = plan.big[0];
+    p.rect[1] = plan.big[1];
     if (acc)
       launch_kernel<TileBig, OP, true>(p, bias, gelu, stream);
     else
       launch_kernel<TileBig, OP, false>(p, bias, gelu, stream);
-  } else {
+  }
+  if (plan.std_rects > 0) {
+    p.n_rect = plan.std_rects;
+    p.rect[0] = plan.std_[0];
+    p.rect[1] = plan.std_[1];
     if (acc)
       launch_kernel<TileStd, OP, true>(p, bias, gelu, stream);
     else
@@ -748,8 +830,8 @@ extern "C" int wf_gemm_set_phase_buffer(uint64_t* stamps) {
 }
 #endif
 #if defined(WF_GEMM_PHASES) || defined(WF_GEMM_TILE_LAB)
-// Instrumented builds only: the workgroup tile of the following GEMM launches (-1 the product's choice,
-// 0 the 128 x 256 tile, 1 the 256 x 256 tile).
+// Instrumented builds only: the tile plan of the following GEMM launches (-1 the product's plan, 0 the
+// 128 x 256 tile over the whole output, 1 the 256 x 256 tile over the whole output).
 extern "C" int wf_gemm_set_tile_policy(int policy) {
   WF_REQUIRE(policy >= -1 && policy <= 1, WF_E_INVALID, "wf_gemm_set_tile_policy: policy %d not in -1..1", policy);
   wf::g_tile_policy = policy;

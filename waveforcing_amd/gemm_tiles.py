@@ -4,14 +4,16 @@ Usage: python -m waveforcing_amd.build --variant gemm_tiles        (on the CPU, 
        python -m waveforcing_amd.gemm_tiles [--fp8] [--block]      (on the GPU)
 
 The instrumented library (libwf_mi355x_gemm_tiles.so, built with -DWF_GEMM_TILE_LAB) has the product's
-kernels plus wf_gemm_set_tile_policy, which forces the workgroup tile of the following launches: 0 the
-128 x 256 tile (three 48 KB LDS stages), 1 the 256 x 256 tile (two 64 KB stages), -1 the product's choice.
-For each Wan-1.3B / 14B linear at 4680 tokens (uniform random int8 operands, or random e4m3 codes with
---fp8) it checks that both tiles give bit-identical outputs (every output's accumulator sees the same MFMAs
-in the same K order; int8 also compares the int32 accumulators) and times them in alternating blocks after a
-second of warm-up, so that both run in the same power and clock state.  With --block it runs, instead, the
-1.3B block's four linears and the whole block (bench.py's workloads) under the product's rule against the
-128-row tile everywhere, alternating.  One JSON line per result.
+kernels plus wf_gemm_set_tile_policy, which forces the tile plan of the following launches: 0 the 128 x 256
+tile (three 48 KB LDS stages) over the whole output, 1 the 256 x 256 tile (two 64 KB stages) over the whole
+output, -1 the product's plan (one of those, or whole rounds of 256 x 256 tiles followed by a launch of
+128 x 256 tiles over the rest).  For each Wan-1.3B / 14B linear at 4680 tokens (uniform random int8
+operands, or random e4m3 codes with --fp8) it checks that the three give bit-identical outputs (every
+output's accumulator sees the same MFMAs in the same K order; int8 also compares the int32 accumulators)
+and times them in alternating blocks after a second of warm-up, so that all run in the same power and clock
+state.  With --block it runs, instead, the 1.3B block's four linears, the 1.3B block and the 14B block
+(bench.py's workloads) under the product's plan against the 128-row tile everywhere, alternating.  One JSON
+line per result.
 """
 
 from __future__ import annotations
@@ -72,22 +74,24 @@ def shapes_ab(fp8: bool, dev: str = "cuda:0") -> None:
             sx = torch.rand((M,), generator=g, device=dev) * 0.01
             sw = torch.rand((N,), generator=g, device=dev) * 0.01
         bias = torch.randn((N,), generator=g, device=dev).to(torch.bfloat16)
-        ys = [torch.full((M, N), 7.0, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-        accs = [None, None] if fp8 else [torch.full((M, N), 7, dtype=torch.int32, device=dev) for _ in range(2)]
-        for pol in (0, 1):
+        pols = (0, 1, -1)
+        ys = {pol: torch.full((M, N), 7.0, dtype=torch.bfloat16, device=dev) for pol in pols}
+        accs = {pol: None if fp8 else torch.full((M, N), 7, dtype=torch.int32, device=dev) for pol in pols}
+        for pol in pols:
             call(pol, a, w, sx, sw, bias, ys[pol], accs[pol])
         torch.cuda.synchronize()
-        same = bool(torch.equal(ys[0], ys[1])) and (fp8 or bool(torch.equal(accs[0], accs[1])))
+        same = all(bool(torch.equal(ys[0], ys[pol])) and (fp8 or bool(torch.equal(accs[0], accs[pol])))
+                   for pol in pols[1:])
         ops = 2.0 * M * N * K
         reps = max(3, int(4e11 / ops))
         t0 = time.time()
         while time.time() - t0 < 1.0:
-            for pol in (0, 1):
+            for pol in pols:
                 call(pol, a, w, sx, sw, bias, ys[pol], None)
             torch.cuda.synchronize()
-        times = {0: [], 1: []}
+        times = {pol: [] for pol in pols}
         for blk in range(6):
-            for pol in ((0, 1) if blk % 2 == 0 else (1, 0)):
+            for pol in (pols if blk % 2 == 0 else pols[::-1]):
                 s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 s.record()
                 for _ in range(reps):
@@ -98,11 +102,13 @@ def shapes_ab(fp8: bool, dev: str = "cuda:0") -> None:
         med = {p: statistics.median(t) for p, t in times.items()}
         print(json.dumps({"shape": name, "M": M, "N": N, "K": K, "fp8": fp8, "bit_identical": same,
                           "tiles_128": -(-M // 128) * -(-N // 256), "tiles_256": -(-M // 256) * -(-N // 256),
-                          "us_128": round(med[0], 2), "us_256": round(med[1], 2),
+                          "us_128": round(med[0], 2), "us_256": round(med[1], 2), "us_plan": round(med[-1], 2),
                           "tops_128": round(ops / med[0] / 1e6, 1), "tops_256": round(ops / med[1] / 1e6, 1),
-                          "ratio_256_over_128": round(med[1] / med[0], 4)}), flush=True)
+                          "tops_plan": round(ops / med[-1] / 1e6, 1),
+                          "ratio_256_over_128": round(med[1] / med[0], 4),
+                          "ratio_plan_over_128": round(med[-1] / med[0], 4)}), flush=True)
         if not same:
-            raise RuntimeError(f"{name}: the two tiles disagree")
+            raise RuntimeError(f"{name}: the tile plans disagree")
         del a, w, ys, accs
 
 
@@ -124,9 +130,11 @@ def block_ab(dev: str = "cuda:0") -> None:
             assert lib.wf_gemm_set_tile_policy(pol) == 0
             lin = bench.bench_block_linears(20, 3, dev)
             blk = bench.bench_block("1.3b", 20, 3, dev)
-            print(json.dumps({"rep": rep, "policy": "product rule" if pol < 0 else "128-row tile",
+            b14 = bench.bench_block("14b", 10, 2, dev)
+            print(json.dumps({"rep": rep, "policy": "product plan" if pol < 0 else "128-row tile",
                               "linears_1p3b_us": round(lin["ms"] * 1e3, 1), "linears_1p3b_tops": round(lin["tops"], 1),
-                              "block_1p3b_ms": round(blk["ms"], 4)}), flush=True)
+                              "block_1p3b_ms": round(blk["ms"], 4), "block_14b_ms": round(b14["ms"], 4)}),
+                  flush=True)
 
 
 def main() -> None:
