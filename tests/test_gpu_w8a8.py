@@ -71,10 +71,6 @@ def _gemm_case(M, N, K, seed, bias=True, gelu=False):
     # (72 rows in the last tile row, a 252-column last tile with N % 8 == 4, a 16-byte K tail), and K loops
     # of one and two steps
     (4680, 8960, 1536), (4680, 8956, 1552), (4680, 8960, 16), (4680, 8960, 144),
-    # shapes planned as whole rounds of 256 x 256 tiles plus a second launch of 128 x 256 tiles over the rest
-    # (on 256 CUs): one round and a partly covered tile row (N = 5120, the 14B O / fc_out), four rounds
-    # (N = 15360, the 14B QKV), three rounds (N = 13824, the 14B fc_in); every output element compared
-    (4680, 5120, 512), (4680, 15360, 256), (4680, 13824, 272),
 ])
 def test_gemm_exact(M, N, K):
     y, acc, oy, oacc = _gemm_case(M, N, K, seed=M + N + K)
@@ -110,6 +106,32 @@ def test_gemm_14b_shapes_sampled_rows(N, K, gelu):
         assert rel < 1e-2, float(rel)
     else:
         assert torch.equal(y[rows], oy)
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (4680, 5120, 4096),    # one round and a partly covered tile row (the 14B O / fc_out plan)
+    (4680, 5112, 4112),    # the same plan with a 248-column last tile and a 16-byte K tail
+    (4680, 15360, 4096),   # four rounds, then the rest (the 14B QKV plan)
+    (4680, 13824, 4096),   # three rounds, then the rest (the 14B fc_in plan)
+])
+def test_gemm_tile_plans_exact(M, N, K):
+    """Shapes planned (on 256 CUs) as whole rounds of 256 x 256 tiles followed by a launch of 128 x 256 tiles
+    over the rest: every element of the int32 accumulators equals torch._int_mm (exact integer products), and
+    every bf16 output equals the epilogue (float(acc) * sx) * sw + bias evaluated by torch in that order, so a
+    tile that no launch covers, or covers twice with different rows, fails.  Outputs start as a fill pattern."""
+    g = torch.Generator(device=DEV).manual_seed(M + N + K)
+    qx = torch.randint(-127, 128, (M, K), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    qw = torch.randint(-127, 128, (N, K), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    sx = torch.rand((M,), generator=g, device=DEV) * 1e-3
+    sw = torch.rand((N,), generator=g, device=DEV) * 1e-3
+    b = torch.randn((N,), generator=g, device=DEV).to(torch.bfloat16)
+    acc = torch.full((M, N), 0x7f7f7f7f, dtype=torch.int32, device=DEV)
+    y = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=DEV)
+    gemm_i8(qx, qw, sx, sw, b, acc_out=acc, out=y)
+    ref = torch._int_mm(qx, qw.t())
+    assert torch.equal(acc, ref)
+    yr = ((ref.float() * sx[:, None]) * sw[None, :] + b.float()[None, :]).to(torch.bfloat16)
+    assert torch.equal(y, yr)
 
 
 def test_gemm_no_bias_exact():

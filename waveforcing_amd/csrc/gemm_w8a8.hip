@@ -621,10 +621,13 @@ int device_cus() {
 // everywhere; the 256-row tile everywhere; or F whole rounds of 256-row tiles (F x CUs of them in row-major
 // order over the 256-row grid: whole tile rows, then a prefix of the next) followed by a second launch of
 // 128-row tiles over the rest (the suffix of that tile row and every row below), so that neither launch
-// ends on a mostly idle round.  The cheapest plan by the model is taken when it costs at least
-// kPlanMargin less than the 128-row tile alone.
+// ends on a mostly idle round.  The second launch has a fixed cost (about 3 us of launch gap and ramp, a
+// third of a 128-row round at K = 1536, under a tenth from K = 4096), so mixed plans are considered from
+// kMixedMinK on.  The cheapest plan by the model is taken when it costs at least kPlanMargin less than the
+// 128-row tile alone.
 constexpr double kBigTileCost = 1.75;
 constexpr double kPlanMargin = 0.95;
+constexpr int kMixedMinK = 4096;
 
 struct Plan {
   int big_rects = 0;  // 0: no 256-row launch
@@ -637,7 +640,7 @@ int64_t rect_tiles(const Rect& r, int bm) {
   return static_cast<int64_t>((r.m1 - r.m0 + bm - 1) / bm) * ((r.n1 - r.n0 + 255) / 256);
 }
 
-Plan plan_tiles(int M, int N) {
+Plan plan_tiles(int M, int N, int K) {
   Plan all_std;
   all_std.std_rects = 1;
   all_std.std_[0] = Rect{0, M, 0, N};
@@ -657,7 +660,7 @@ Plan plan_tiles(int M, int N) {
     best = all_big;
     best_cost = cost_big;
   }
-  for (int64_t f = 1; f * cus < big_tiles; ++f) {
+  for (int64_t f = 1; K >= kMixedMinK && f * cus < big_tiles; ++f) {
     const int64_t nb = f * cus;
     const int full = static_cast<int>(nb / tn), part = static_cast<int>(nb % tn);
     Plan pl;
@@ -685,7 +688,7 @@ Plan plan_tiles(int M, int N) {
 template <typename OP>
 int launch(const GemmArgs& p0, bool bias, bool gelu, hipStream_t stream, const char* fn) {
   const bool acc = std::is_same<OP, OpI8>::value && p0.acc_out != nullptr;
-  const Plan plan = plan_tiles(p0.M, p0.N);
+  const Plan plan = plan_tiles(p0.M, p0.N, p0.K);
   GemmArgs p = p0;
   if (plan.big_rects > 0) {
     p.n_rect = plan.big_rects;
