@@ -1,6 +1,6 @@
 """Build libwf_mi355x.so from csrc/*.hip with hipcc for gfx950.
 
-Usage: python -m waveforcing_amd.build [--jobs N] [--verbose] [--variant gemm_phases|gemm_tiles]
+Usage: python -m waveforcing_amd.build [--jobs N] [--verbose] [--variant gemm_phases|gemm_tiles|hbm_probe]
 
 Every translation unit is compiled to an object under waveforcing_amd/_build/
 in parallel, then linked into waveforcing_amd/libwf_mi355x.so (in-tree, so it
@@ -11,8 +11,10 @@ call always rebuilds.
 libwf_mi355x_gemm_phases.so, whose W8A8 GEMM records shader-clock stamps of its
 phases (waveforcing_amd/gemm_phases.py reads them); ``--variant gemm_tiles``
 builds libwf_mi355x_gemm_tiles.so, whose GEMM tile can be forced per launch
-(wf_gemm_set_tile_policy, for A/B runs of the two workgroup tiles).  The
-product library is built with neither.
+(wf_gemm_set_tile_policy, for A/B runs of the two workgroup tiles);
+``--variant hbm_probe`` builds libwf_mi355x_hbm_probe.so with a bare 2 : 1
+read : write stream kernel (wf_probe_stream_2to1, read by
+waveforcing_amd/hbm_ceiling.py).  The product library is built with none.
 """
 
 from __future__ import annotations
@@ -32,7 +34,7 @@ LIB_NAME = "libwf_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = "gfx950"
 # instrumented variants: name -> extra compile flags (their own object directory and library name)
-VARIANTS = {"gemm_phases": ["-DWF_GEMM_PHASES"], "gemm_tiles": ["-DWF_GEMM_TILE_LAB"]}
+VARIANTS = {"gemm_phases": ["-DWF_GEMM_PHASES"], "gemm_tiles": ["-DWF_GEMM_TILE_LAB"], "hbm_probe": ["-DWF_HBM_PROBE"]}
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
