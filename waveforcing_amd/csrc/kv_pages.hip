@@ -675,10 +675,12 @@ int wf_fp8_kv_unpack(const uint8_t* k_codes, const uint8_t* v_codes, const float
 }  // extern "C"
 
 #ifdef WF_HBM_PROBE
-// Instrumented build only (not declared in wf_api.h): the HBM ceiling for the pack's traffic mix.  Each
-// thread reads 16 bytes and writes 8 per iteration (the high bytes of eight bf16, a stand-in for the pack's
-// 2 : 1 read : write ratio), fully coalesced, grid-stride over n 16-byte items; `nontemporal` marks the stores
-// as streaming.  waveforcing_amd/hbm_ceiling.py sweeps the grid and times it beside the pack.
+// Instrumented build only (not declared in wf_api.h): the HBM ceilings for the pack's and the unpack's traffic
+// mixes.  wf_probe_stream_2to1: each thread reads 16 bytes and writes 8 per iteration (the high bytes of eight
+// bf16, a stand-in for the pack's 2 : 1 read : write ratio), fully coalesced, grid-stride over n 16-byte
+// items; wf_probe_stream_1to2: reads 8 and writes 16 (eight bytes widened to bf16 high bytes, the unpack's
+// 1 : 2); `nontemporal` marks the stores as streaming.  waveforcing_amd/hbm_ceiling.py sweeps the grid and
+// times them beside the pack and the unpack.
 namespace wf {
 namespace {
 template <bool NT>
@@ -696,8 +698,39 @@ __global__ __launch_bounds__(256) void stream_2to1_kernel(const uint4* __restric
       *reinterpret_cast<u2v*>(dst + i) = w;
   }
 }
+template <bool NT>
+__global__ __launch_bounds__(256) void stream_1to2_kernel(const uint2* __restrict__ src, uint4* __restrict__ dst,
+                                                          int64_t n) {
+  typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+    const uint2 v = src[i];
+    const u4v w = {(v.x & 0xffu) << 8 | (v.x & 0xff00u) << 16, (v.x >> 8 & 0xff00u) | (v.x & 0xff000000u),
+                   (v.y & 0xffu) << 8 | (v.y & 0xff00u) << 16, (v.y >> 8 & 0xff00u) | (v.y & 0xff000000u)};
+    if constexpr (NT)
+      __builtin_nontemporal_store(w, reinterpret_cast<u4v*>(dst) + i);
+    else
+      *reinterpret_cast<u4v*>(dst + i) = w;
+  }
+}
 }  // namespace
 }  // namespace wf
+
+extern "C" int wf_probe_stream_1to2(const void* src, void* dst, int64_t n, int32_t grid, int32_t nontemporal,
+                                    void* stream) {
+  WF_REQUIRE(src && dst && n > 0 && grid > 0, WF_E_INVALID, "wf_probe_stream_1to2: bad arguments");
+  WF_REQUIRE((reinterpret_cast<uintptr_t>(src) & 7u) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0,
+             WF_E_ALIGN, "wf_probe_stream_1to2: src must be 8-byte and dst 16-byte aligned");
+  const auto* s = static_cast<const uint2*>(src);
+  auto* d = static_cast<uint4*>(dst);
+  if (nontemporal)
+    hipLaunchKernelGGL(wf::stream_1to2_kernel<true>, dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
+                       wf::as_stream(stream), s, d, n);
+  else
+    hipLaunchKernelGGL(wf::stream_1to2_kernel<false>, dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
+                       wf::as_stream(stream), s, d, n);
+  return wf::check_launch("wf_probe_stream_1to2");
+}
 
 extern "C" int wf_probe_stream_2to1(const void* src, void* dst, int64_t n, int32_t grid, int32_t nontemporal,
                                     void* stream) {

@@ -1,15 +1,15 @@
-"""The HBM ceiling for the FP8 KV pack's traffic mix, from the instrumented build.
+"""The HBM ceilings for the FP8 KV pack's and unpack's traffic mixes, from the instrumented build.
 
 Usage: python -m waveforcing_amd.build --variant hbm_probe      (on the CPU, once)
        python -m waveforcing_amd.hbm_ceiling [--reps R]          (on the GPU)
 
 The instrumented library (libwf_mi355x_hbm_probe.so, built with -DWF_HBM_PROBE) holds the product's kernels
-plus wf_probe_stream_2to1: a bare grid-stride stream that reads 16 bytes and writes 8 per thread and
-iteration, fully coalesced, with plain or nontemporal stores: the pack's 2 : 1 read : write ratio with no
-other work.  Over the pack workload's 862.6 MB of input (30 layers of K and V, [4680, 12, 128] bf16) it
-sweeps the grid size, then times the 30-layer pack itself in the same process, each after a second of
-sustained launches, R times in alternation.  One JSON line per measurement; GB/s count bytes read plus
-written.
+plus wf_probe_stream_2to1 / wf_probe_stream_1to2: bare grid-stride streams that read 16 bytes and write 8
+(or read 8 and write 16) per thread and iteration, fully coalesced, with plain or nontemporal stores: the
+pack's 2 : 1 and the unpack's 1 : 2 read : write ratios with no other work.  Over the pack workload's
+862.6 MB of bf16 (30 layers of K and V, [4680, 12, 128]) and its 431.3 MB of codes it sweeps the grid size,
+then times the 30-layer pack and unpack themselves in the same process, each after a second of sustained
+launches, R times in alternation.  One JSON line per measurement; GB/s count bytes read plus written.
 """
 
 from __future__ import annotations
@@ -39,6 +39,7 @@ def main() -> None:
     lib = _lib.load()
     vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
     lib.wf_probe_stream_2to1.argtypes = [vp, vp, i64, i32, i32, vp]
+    lib.wf_probe_stream_1to2.argtypes = [vp, vp, i64, i32, i32, vp]
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     import bench
 
@@ -48,24 +49,28 @@ def main() -> None:
     dst = torch.empty((in_bytes // 2,), dtype=torch.uint8, device=dev)
     stream = _lib.stream_handle(dev)
 
-    def stream_call(grid, nt):
-        rc = lib.wf_probe_stream_2to1(src.data_ptr(), dst.data_ptr(), n, grid, nt, stream)
+    def stream_call(fn, a, b, grid, nt):
+        rc = fn(a.data_ptr(), b.data_ptr(), n, grid, nt, stream)
         if rc != 0:
-            raise RuntimeError(f"wf_probe_stream_2to1 failed with status {rc}")
+            raise RuntimeError(f"stream probe failed with status {rc}")
 
     for rep in range(args.reps):
-        best = 0.0
-        for nt in (0, 1):
-            for grid in GRIDS:
-                ms = bench._timed(lambda: stream_call(grid, nt), 20, 3, 1.0)
-                gbs = 24.0 * n / (ms * 1e-3) / 1e9
-                best = max(best, gbs)
-                print(json.dumps({"rep": rep, "kernel": "stream_2to1", "nontemporal": nt, "grid": grid,
-                                  "us": round(ms * 1e3, 1), "gbs": round(gbs, 1)}), flush=True)
-        kv = bench.bench_kv(20, 3, dev, ("pack",))
-        print(json.dumps({"rep": rep, "kernel": "kv_pack 30 layers", "us": round(kv["ms_pack"] * 1e3, 1),
-                          "gbs": round(kv["pack_gbs"], 1), "stream_2to1_best_gbs": round(best, 1),
-                          "pack_over_stream": round(kv["pack_gbs"] / best, 4)}), flush=True)
+        best = {}
+        for name, fn, a, b in (("stream_2to1", lib.wf_probe_stream_2to1, src, dst),
+                               ("stream_1to2", lib.wf_probe_stream_1to2, dst, src)):
+            best[name] = 0.0
+            for nt in (0, 1):
+                for grid in GRIDS:
+                    ms = bench._timed(lambda: stream_call(fn, a, b, grid, nt), 20, 3, 1.0)
+                    gbs = 24.0 * n / (ms * 1e-3) / 1e9
+                    best[name] = max(best[name], gbs)
+                    print(json.dumps({"rep": rep, "kernel": name, "nontemporal": nt, "grid": grid,
+                                      "us": round(ms * 1e3, 1), "gbs": round(gbs, 1)}), flush=True)
+        kv = bench.bench_kv(20, 3, dev, ("pack", "unpack"))
+        for op, key in (("pack", "stream_2to1"), ("unpack", "stream_1to2")):
+            print(json.dumps({"rep": rep, "kernel": f"kv_{op} 30 layers", "us": round(kv[f"ms_{op}"] * 1e3, 1),
+                              "gbs": round(kv[f"{op}_gbs"], 1), f"{key}_best_gbs": round(best[key], 1),
+                              "over_stream": round(kv[f"{op}_gbs"] / best[key], 4)}), flush=True)
 
 
 if __name__ == "__main__":
