@@ -631,9 +631,9 @@ constexpr int kMixedMinK = 4096;
 
 struct Plan {
   int big_rects = 0;  // 0: no 256-row launch
-  Rect big[2];
+  Rect big[2] = {};
   int std_rects = 0;  // 0: no 128-row launch
-  Rect std_[2];
+  Rect std_[2] = {};
 };
 
 int64_t rect_tiles(const Rect& r, int bm) {
