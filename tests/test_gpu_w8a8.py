@@ -134,6 +134,33 @@ def test_gemm_tile_plans_exact(M, N, K):
     assert torch.equal(y, yr)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_gemm_random_large_shapes_exact(seed):
+    """Seeded large shapes (M 1500-9000, N 3200-17600 in steps of 8, K 4096-6384 in steps of 16) that the
+    planner splits in several ways (the 256-row tile over the whole output, or whole rounds of it followed by
+    128-row tiles over rectangles with ragged row and column ends): int32 accumulators equal torch._int_mm
+    and bf16 outputs equal the torch-evaluated epilogue, element for element."""
+    import random
+
+    r = random.Random(seed)
+    M, N, K = r.randrange(1500, 9000), 8 * r.randrange(400, 2200), 16 * r.randrange(256, 400)
+    print(f"seed {seed}: {M} x {N} x {K}")
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    qx = torch.randint(-127, 128, (M, K), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    qw = torch.randint(-127, 128, (N, K), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    sx = torch.rand((M,), generator=g, device=DEV) * 1e-3
+    sw = torch.rand((N,), generator=g, device=DEV) * 1e-3
+    b = torch.randn((N,), generator=g, device=DEV).to(torch.bfloat16)
+    acc = torch.full((M, N), 0x7f7f7f7f, dtype=torch.int32, device=DEV)
+    y = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=DEV)
+    gemm_i8(qx, qw, sx, sw, b, acc_out=acc, out=y)
+    ref = torch._int_mm(qx, qw.t())
+    assert torch.equal(acc, ref)
+    del acc
+    yr = ((ref.float() * sx[:, None]) * sw[None, :] + b.float()[None, :]).to(torch.bfloat16)
+    assert torch.equal(y, yr)
+
+
 def test_gemm_no_bias_exact():
     y, acc, oy, oacc = _gemm_case(700, 384, 512, seed=3, bias=False)
     assert torch.equal(acc, oacc) and torch.equal(y, oy)
