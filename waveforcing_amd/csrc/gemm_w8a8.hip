@@ -63,6 +63,7 @@
 // (s_memtime, wave 0) and the 100 MHz reference clock (s_memrealtime, wave 4) into a buffer registered
 // with wf_gemm_set_phase_buffer: 8 stamps per workgroup, [wave 0: 4][wave 4: 4].  waveforcing_amd/gemm_phases.py builds that variant and summarizes the
 // stamps (prologue, cycles per K step, epilogue).
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -602,17 +603,19 @@ void launch_kernel(const GemmArgs& p, bool bias, bool gelu, hipStream_t stream) 
 // in the instrumented libraries, for A/B runs).
 int g_tile_policy = -1;
 
-// Compute units of the current device (one workgroup per CU at a time), cached per device.
+// Compute units of the current device (one workgroup per CU at a time), cached per device (host threads may
+// call concurrently; each stores the same value).
 int device_cus() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
+  int v = cus[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     int n = 0;
-    cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n
-                                                                                                             : 256;
+    v = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
+    cus[dev].store(v, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return v;
 }
 
 // Both tiles run one workgroup per CU, so a launch takes about ceil(tiles / CUs) rounds of its tile's time.
