@@ -86,7 +86,6 @@ def sdpa_qk8(q, k_codes, k_scales, v, scale=None) -> torch.Tensor:
 
 LOG2E = 1.4426950408889634
 TILE_KEYS = 64      # keys per step of the fp8-PV form
-WAVE_QUERIES = 32   # queries that share one lazy-rescale decision
 RESCALE_TAU = 8.0   # lazy-rescale threshold (log2 units)
 
 
@@ -123,11 +122,11 @@ def sdpa_qkpv8(q, k_codes, k_scales, v_codes, v_scales, scale=None, round_p: boo
     """Attention with e4m3 queries and e4m3 weights over K/V codes [Lk, H, D] (uint8) with scales [Lk, H].
 
     The weights are formed as the HIP kernel forms them, step by step, so that their e4m3 rounding sees the same
-    values: keys in tiles of 64, queries in groups of 32 that share the lazy-rescale decision.  Scores
+    values: keys in tiles of 64, each query with its own lazy maximum.  Scores
     s = (sum_d code_q code_k) s_q with u_k = fp32(s_k * fp32(scale * log2 e)); per tile and query the bound
     max(s) * max(0, max u) over each half of the tile's keys (the keys whose index has bit 2 clear / set; 0 when
-    the half's max(s) < 0), and when any bound of the group exceeds its threshold, every query of the group
-    takes m = max(m, max_k fp32(s u_k)) with O and l scaled by 2^(m_old - m) and threshold m + 8.  Then
+    the half's max(s) < 0), and a query whose bound exceeds its threshold takes m = max(m, max_k fp32(s u_k))
+    with O and l scaled by 2^(m_old - m) and threshold m + 8.  Then
     p_k = 2^fp32(s u_k - m), l += p_k, w_k = fp32(p_k s_v,k); 2^E from the tile's max w (:func:`pv8_exponent`);
     O += sum_k e4m3(w_k / 2^E) 2^E code_v,k.  Out: O / l.  With ``round_p`` False the weights are not rounded,
     which leaves the quantized-QK attention of :func:`sdpa_qk8` over the dequantized V.
@@ -147,27 +146,25 @@ def sdpa_qkpv8(q, k_codes, k_scales, v_codes, v_scales, scale=None, round_p: boo
     margin = torch.zeros_like(out)
     if n_kv == 0:
         return (out.float(), margin.float()) if margin_eps is not None else out.float()
-    Qp = -(-Lq // WAVE_QUERIES) * WAVE_QUERIES
     n_tiles = -(-n_kv // TILE_KEYS)
     Kp = n_tiles * TILE_KEYS
     half = ((torch.arange(TILE_KEYS) >> 2) & 1).bool()              # bit 2 of the key index in its tile
     kcf = k_codes.view(okv.FP8).float().double()
     vcf = v_codes.view(okv.FP8).float().double()
     for h in range(H):
-        s = torch.full((Qp, Kp), -math.inf, dtype=torch.float64)
-        s[:Lq, :n_kv] = _f32((qc[:, h].double() @ kcf[:, h].T) * sq[:, h, None].double())
-        s[Lq:, :n_kv] = 0.0                                           # query rows past Lq are zero queries
+        s = torch.full((Lq, Kp), -math.inf, dtype=torch.float64)
+        s[:, :n_kv] = _f32((qc[:, h].double() @ kcf[:, h].T) * sq[:, h, None].double())
         u = torch.ones(Kp, dtype=torch.float64)
         u[:n_kv] = _f32(k_scales[:, h].float().double() * c32)
         sv = torch.zeros(Kp, dtype=torch.float64)
         sv[:n_kv] = v_scales[:, h].float().double()
         vh = torch.zeros((Kp, D), dtype=torch.float64)
         vh[:n_kv] = vcf[:, h]
-        m = torch.full((Qp,), -math.inf, dtype=torch.float64)
-        thr = torch.full((Qp,), -math.inf, dtype=torch.float64)
-        o = torch.zeros((Qp, D), dtype=torch.float64)
-        amb = torch.zeros((Qp, D), dtype=torch.float64)
-        l = torch.zeros(Qp, dtype=torch.float64)
+        m = torch.full((Lq,), -math.inf, dtype=torch.float64)
+        thr = torch.full((Lq,), -math.inf, dtype=torch.float64)
+        o = torch.zeros((Lq, D), dtype=torch.float64)
+        amb = torch.zeros((Lq, D), dtype=torch.float64)
+        l = torch.zeros(Lq, dtype=torch.float64)
         for t in range(n_tiles):
             ks = slice(t * TILE_KEYS, (t + 1) * TILE_KEYS)
             st, ut = s[:, ks], u[ks]
@@ -177,7 +174,7 @@ def sdpa_qkpv8(q, k_codes, k_scales, v_codes, v_scales, scale=None, round_p: boo
                 um = max(0.0, float(ut[hm].max()))
                 b = torch.where(mt >= 0, _f32(mt * um), torch.zeros_like(mt))
                 bound = b if bound is None else torch.maximum(bound, b)
-            fire = (bound > thr).view(-1, WAVE_QUERIES).any(dim=1).repeat_interleave(WAVE_QUERIES)
+            fire = bound > thr
             if bool(fire.any()):
                 ex = _f32(st * ut[None, :]).amax(dim=1)
                 m_new = torch.maximum(m, ex)
@@ -202,6 +199,6 @@ def sdpa_qkpv8(q, k_codes, k_scales, v_codes, v_scales, scale=None, round_p: boo
                 w = y.float().to(okv.FP8).double() * sc
             o += w @ vh[ks]
         res = torch.where(l[:, None] > 0, o / l[:, None], torch.zeros_like(o))
-        out[:, h] = res[:Lq]
-        margin[:, h] = torch.where(l[:, None] > 0, amb / l[:, None], torch.zeros_like(amb))[:Lq]
+        out[:, h] = res
+        margin[:, h] = torch.where(l[:, None] > 0, amb / l[:, None], torch.zeros_like(amb))
     return (out.float(), margin.float()) if margin_eps is not None else out.float()

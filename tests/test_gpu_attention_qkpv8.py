@@ -8,9 +8,8 @@ e4m3 weights tile by tile as the kernel does) under the attention bar, |out - or
 bound on what weights lying within a relative 2^-15 of an e4m3 rounding midpoint can move an output by when
 they round the other way: the kernel's fp32 scores (the matrix cores' own accumulation) and exponentials
 (v_exp_f32) differ from the oracle's in the last bits, and near a midpoint that decides the rounding; one
-such weight moves a row of a short context by up to a few percent.  The oracle groups queries in runs of 32
-from its first row (the queries that share a lazy-rescale decision in the kernel), so sampled rows are passed
-to it in 32-aligned blocks.  The distance from the exact attention (oracle.attention.paged_fp8) is printed
+such weight moves a row of a short context by up to a few percent.  Each query keeps its own lazy maximum in
+the kernel as in the oracle, so any sample of rows can be passed to the oracle.  The distance from the exact attention (oracle.attention.paged_fp8) is printed
 next to it: the approximation the form makes.
 """
 
@@ -57,9 +56,7 @@ def _setup(Lq, H, n_kv, page, P, seed, heavy=False, k=None, v=None, q=None):
 
 
 def _oracle_blocks(q, blocks, kp, vp, ids, n_kv, page):
-    """The oracle over row blocks [a, b) of q, concatenated: each block starts at a multiple of 32 and all but
-    the last hold whole groups of 32, so the oracle's groups are the kernel's."""
-    assert all(a % 32 == 0 for a, _ in blocks) and all((b - a) % 32 == 0 for a, b in blocks[:-1])
+    """The oracle over row blocks [a, b) of q, concatenated."""
     return oat.paged_fp8_qkpv8(torch.cat([q[a:b] for a, b in blocks], 0), kp, vp, ids, n_kv, page, margin_eps=EPS)
 
 
@@ -98,13 +95,13 @@ def test_qkpv8_heavy_tailed_relative():
 
 @pytest.mark.parametrize("H,seed", [(12, 10), (40, 50)])
 def test_qkpv8_full_context_sampled_waves(H, seed):
-    """4680 queries over 8 chunks (37440 keys); five 32-query groups (the first two, the last partial one and
-    two drawn at random), all heads."""
+    """4680 queries over 8 chunks (37440 keys); five blocks of rows (the first 64, the partial last wave, two
+    32-row waves drawn at random and 19 rows straddling two waves), all heads."""
     Lq, n_kv, page = 4680, 37440, 1560
     q, ctx, ids, kp, vp = _setup(Lq, H, n_kv, page, 26 if H == 40 else 30, seed=seed)
     out = attn_paged_fp8_qkpv(q.to(DEV), ctx).cpu().float()
     picks = torch.randperm(Lq // 32 - 3, generator=torch.Generator().manual_seed(seed))[:2] + 2
-    blocks = [(0, 64)] + [(32 * int(w), 32 * int(w) + 32) for w in picks] + [(Lq // 32 * 32, Lq)]
+    blocks = [(0, 64)] + [(32 * int(w), 32 * int(w) + 32) for w in picks] + [(2000, 2019), (Lq // 32 * 32, Lq)]
     ref, margin = _oracle_blocks(q, blocks, kp, vp, ids, n_kv, page)
     got = torch.cat([out[a:b] for a, b in blocks], 0)
     exact = oat.paged_fp8(torch.cat([q[a:b] for a, b in blocks], 0), kp, vp, ids, n_kv, page)

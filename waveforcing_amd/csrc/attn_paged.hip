@@ -43,10 +43,12 @@
 // the vector work only hides when it sits between the wave's own MFMAs.
 //
 // Softmax in base 2 with the scale folded into one FMA per score, and lazy
-// rescaling: the running maximum used in the exponent is raised only when a
-// tile's maximum exceeds it by more than kTau (log2 units), so P <= 2^kTau
-// and the O / row-sum rescale is rare; the final normalisation divides by
-// the row sum taken against the same maximum, so the result is unchanged.
+// rescaling: a query's running maximum used in the exponent is raised only
+// when its tile maximum exceeds it by more than kTau (log2 units), so
+// P <= 2^kTau and the O / row-sum rescale is rare; the final normalisation
+// divides by the row sum taken against the same maximum, so the result is
+// unchanged.  The decision is per query, so every output row depends only on
+// its own query and the context.
 // K stays exactly bf16(code * s): with heavy-tailed K the scores reach
 // magnitudes where any further rounding of K (e.g. folding the scale into
 // it) moves P by percents.
@@ -632,8 +634,11 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
       mt = mt >= 0.f ? mt * um : 0.f;
     }
     mt = pair_max(mt);
-    // exponents in base 2: p = 2^(c * (s - m_use)), c = softmax_scale * log2(e) >= 0 (QK8: 2^(s'' u_k - m_use))
-    if (__ballot(mt > m_thr)) {
+    // exponents in base 2: p = 2^(c * (s - m_use)), c = softmax_scale * log2(e) >= 0 (QK8: 2^(s'' u_k - m_use)).
+    // Each query decides for itself (the wave only branches when one of its queries rescales), so a query's
+    // output does not depend on which queries share its wave.
+    const bool fire = mt > m_thr;
+    if (__ballot(fire)) {
       if constexpr (QK8) {
         float ex = -INFINITY;
 #pragma unroll
@@ -642,8 +647,9 @@ __global__ __launch_bounds__(THREADS, 1) void attn_paged_fp8_kernel(AttnArgs p) 
           for (int e = 0; e < 16; ++e) ex = fmaxf(ex, s[b][e] * u[b][e]);
         mt = pair_max(ex);
       }
-      const float m_new = fmaxf(m_use, mt);
-      const float alpha = (m_use == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(c * (m_use - m_new));
+      const float m_new = fire ? fmaxf(m_use, mt) : m_use;
+      const float alpha =
+          !fire ? 1.f : (m_use == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(c * (m_use - m_new));
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] *= alpha;
       l_run *= alpha;
