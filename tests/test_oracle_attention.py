@@ -157,8 +157,8 @@ def _exact_v(vc, vs):
 
 
 def test_qkpv8_without_weight_rounding_is_the_quantized_qk_form():
-    """With the weights left unrounded the tile-by-tile evaluation (lazy maxima shared by groups of 32 queries,
-    rescaled sums, masked tail keys) must give the quantized-QK attention of the definition over V = code * s.
+    """With the weights left unrounded the tile-by-tile evaluation (each query's lazy maximum, rescaled sums,
+    masked tail keys) must give the quantized-QK attention of the definition over V = code * s.
     Later tiles carry keys scaled up 3x per tile, so the running maxima move by far more than the rescale
     threshold and the rescale path runs."""
     for Lq, H, n, seed in ((70, 2, 200, 0), (33, 1, 64, 1), (5, 1, 65, 2), (100, 2, 1, 3), (40, 1, 300, 4)):
@@ -173,6 +173,23 @@ def test_qkpv8_without_weight_rounding_is_the_quantized_qk_form():
         assert (got - want).abs().max().item() < 1e-4, (Lq, H, n)    # fp32 exponents against float64 ones
         rounded = oat.sdpa_qkpv8(q, kc, ks, vc, vs)
         assert 0 < (rounded - want).abs().max().item() < 0.2
+
+
+def test_qkpv8_rows_are_independent():
+    """Each query keeps its own lazy maximum, as the kernel does: rows evaluated alone, or in another order,
+    give the same values as in one call.  Keys grow 3x per tile and every other query is scaled down 64x, so
+    the rescale path runs for the large queries while the small ones keep their maxima."""
+    Lq, H, n = 45, 2, 300
+    q, k, v = _rand((Lq, H, 128), 50), _rand((n, H, 128), 51), _rand((n, H, 128), 52)
+    q = (q.float() * torch.where(torch.arange(Lq) % 2 == 0, 1.0, 1.0 / 64)[:, None, None]).to(torch.bfloat16)
+    k = (k.float() * torch.pow(3.0, (torch.arange(n) // 64).float())[:, None, None]).to(torch.bfloat16)
+    kc, ks = _codes_and_scales(k)
+    vc, vs = _codes_and_scales(v)
+    full = oat.sdpa_qkpv8(q, kc, ks, vc, vs)
+    perm = torch.randperm(Lq, generator=torch.Generator().manual_seed(53))
+    assert torch.equal(oat.sdpa_qkpv8(q[perm], kc, ks, vc, vs), full[perm])
+    for r in (0, 17, 44):
+        assert torch.equal(oat.sdpa_qkpv8(q[r:r + 1], kc, ks, vc, vs)[0], full[r])
 
 
 def _round4(x: float) -> float:
