@@ -12,7 +12,9 @@ kernel has and a plausible indexing mistake breaks:
   gather-dequant values bf16(code * s), which the unpack kernel produces bit-exactly against the oracle):
   the decode inside the attention kernel is exactly the unpack's;
 * query rows and heads are independent: a slice of query rows starting off any tile boundary, and one head
-  packed alone into a one-head pool, reproduce the full call's rows and head bit for bit.
+  packed alone into a one-head pool, reproduce the full call's rows and head bit for bit; with keys that grow
+  from tile to tile and queries of mixed magnitude, so that some queries of a wave rescale and others do not,
+  rows in another order or alone still reproduce theirs (each query keeps its own running maximum).
 """
 
 import pytest
@@ -34,9 +36,9 @@ def _normal(shape, seed):
     return torch.randn(shape, generator=g, device=DEV).to(torch.bfloat16)
 
 
-def _context(k, v, pool_pages, seed, heads=H):
-    n_pages = -(-k.shape[0] // PAGE)
-    pool = Fp8PagePool(pool_pages, heads, D, PAGE, DEV)
+def _context(k, v, pool_pages, seed, heads=H, page=PAGE):
+    n_pages = -(-k.shape[0] // page)
+    pool = Fp8PagePool(pool_pages, heads, D, page, DEV)
     table = pool.page_table(inputs.page_table(n_pages, pool_pages, seed=seed))
     pool.pack(k, v, table)
     return PagedKV(pool, table, k.shape[0])
@@ -93,3 +95,24 @@ def test_one_head_alone_equals_its_head_of_the_full_call(full, form):
     one = _context(k[:, h:h + 1].contiguous(), v[:, h:h + 1].contiguous(), N_KV // PAGE + 3, seed=905, heads=1)
     out = attn_paged_fp8(q[:, h:h + 1].contiguous(), one, **FORMS[form])
     assert torch.equal(out[:, 0], outs[form][:, h])
+
+
+@pytest.mark.parametrize("form", list(FORMS))
+def test_rows_are_independent_when_some_queries_rescale(form):
+    """Keys from the eleventh 64-key tile on are 4x larger and the first half of the queries is scaled down
+    64x: a large query's scores there exceed its running maximum by more than the rescale threshold (2^8 in
+    the weights), a small query's never do (its softmax stays nearly flat, so a moved maximum would show in
+    the rounding of its weights).  In the full call the small queries fill waves of their own; in a shuffled
+    order they share waves with large ones.  Rows computed in that order, or as a slice across a wave of each
+    kind, still equal their rows of the full call bit for bit."""
+    Lq, h, n_kv, page = 600, 2, 64 * 20 + 9, 200
+    q = _normal((Lq, h, D), 960)
+    q = q * torch.where(torch.arange(Lq, device=DEV) < Lq // 2, 1.0 / 64, 1.0)[:, None, None].to(torch.bfloat16)
+    grow = torch.where(torch.arange(n_kv, device=DEV) >= 640, 4.0, 1.0)[:, None, None]
+    k = (_normal((n_kv, h, D), 961).float() * grow).to(torch.bfloat16)
+    v = _normal((n_kv, h, D), 962)
+    ctx = _context(k, v, -(-n_kv // page) + 3, seed=963, heads=h, page=page)
+    full = attn_paged_fp8(q, ctx, **FORMS[form])
+    perm = torch.randperm(Lq, generator=torch.Generator().manual_seed(964)).to(DEV)
+    assert torch.equal(attn_paged_fp8(q[perm].contiguous(), ctx, **FORMS[form]), full[perm])
+    assert torch.equal(attn_paged_fp8(q[270:351], ctx, **FORMS[form]), full[270:351])
