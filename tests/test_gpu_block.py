@@ -24,6 +24,10 @@ so the GPU block is held to the block bar against the true closed form and
 must sit at least 3x closer to it than to the closed form of any wrong
 wiring (each >= 5 % away); the probe's text K/V must equal their closed
 forms bit for bit.
+
+Page placement is invisible to the block: the whole 1.3B chunk with its
+context and its own pages at other physical pages of a larger pool gives the
+same output and the same packed K/V bits, through each attention form.
 """
 
 import pytest
@@ -165,3 +169,38 @@ def test_block_wiring_probes(kind):
         rel = ((got.double() - want.double()).norm() / want.double().norm()).item()
         print(f"ffn_mod probe rel L2 {rel:.3e}")
         assert rel <= 1e-2 and (got.double() - want.double()).abs().max() <= 5e-2 * want.double().abs().max()
+
+
+@pytest.mark.parametrize("form", list(_FORMS))
+def test_block_output_is_independent_of_page_placement(form):
+    """The whole 1.3B chunk over 7 prior chunks, run twice with the context and the chunk's own pages at other
+    physical pages of a larger pool: the block output and the chunk's packed K/V pages are the same bits."""
+    frames, h, w, heads = 3, 30, 52, 12
+    c = _case(1536, heads, 8960, frames, h, w, prior_chunks=7, text_len=512, seed=16)
+    blk = QuantizedWanBlock(c["params"], heads, DEV)
+    tk, tv = blk.text_kv(c["context"].to(DEV))
+    cos, sin = rope.cos_sin(frames, h, w, c["start_frame"], device=DEV)
+    n_prior_pages = len(c["prior_ids"])
+    results = []
+    for P, seed in ((c["P"], None), (c["P"] + 9, 17)):
+        if seed is None:
+            prior_ids, own_ids = c["prior_ids"], c["own_ids"]
+        else:
+            ids = torch.randperm(P, generator=torch.Generator().manual_seed(seed)).tolist()
+            prior_ids, own_ids = ids[:n_prior_pages], ids[n_prior_pages:n_prior_pages + frames]
+        pool = Fp8PagePool(P, heads, 128, c["page"], DEV)
+        pool.pack(c["prior_k"].to(DEV), c["prior_v"].to(DEV), pool.page_table(prior_ids))
+        x = c["x"].to(DEV).clone()
+        saved = dict(_WAVE_STATE)
+        try:
+            _FORMS[form][0]()
+            blk.forward(x, c["e"].to(DEV), cos, sin, pool, pool.page_table(prior_ids + own_ids),
+                        pool.page_table(own_ids), c["n_ctx"], (tk, tv))
+        finally:
+            _WAVE_STATE.clear()
+            _WAVE_STATE.update(saved)
+        results.append((x, [t[own_ids].clone() for t in (pool.k_codes, pool.v_codes, pool.k_scales, pool.v_scales)]))
+        del pool
+    (x0, own0), (x1, own1) = results
+    assert torch.equal(x0, x1)
+    assert all(torch.equal(a, b) for a, b in zip(own0, own1))
