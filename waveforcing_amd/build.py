@@ -12,8 +12,8 @@ libwf_mi355x_gemm_phases.so, whose W8A8 GEMM records shader-clock stamps of its
 phases (waveforcing_amd/gemm_phases.py reads them); ``--variant gemm_tiles``
 builds libwf_mi355x_gemm_tiles.so, whose GEMM tile can be forced per launch
 (wf_gemm_set_tile_policy, for A/B runs of the two workgroup tiles);
-``--variant hbm_probe`` builds libwf_mi355x_hbm_probe.so with a bare 2 : 1
-read : write stream kernel (wf_probe_stream_2to1, read by
+``--variant hbm_probe`` builds libwf_mi355x_hbm_probe.so with bare 2 : 1 and
+1 : 2 read : write stream kernels (wf_probe_stream_2to1 / _1to2, read by
 waveforcing_amd/hbm_ceiling.py).  The product library is built with none.
 """
 
